@@ -1,0 +1,99 @@
+/*
+ * muon_polar.h — C ABI of the MI355X (gfx950) Polar Express step.
+ *
+ * One Polar Express (Newton-Schulz) iteration of the Muon optimizer:
+ *
+ *     A = X·Xᵀ          (stage 1, "gram":  symmetric SYRK, upper tiles + mirror)
+ *     P = b·A + c·A·A   (stage 2, "poly":  A·A with the polynomial in the epilogue)
+ *     Y = a·X + P·X     (stage 3, "apply": P·X with the a·X add in the epilogue)
+ *
+ * X and Y are row-major contiguous bf16 tensors of shape [batch, m, n] with
+ * 1 <= m <= n.  A and P live in a caller-provided scratch ("workspace") of
+ * shape [batch, padded_rows, padded_rows] each, where padded_rows >= m is the
+ * stage tile multiple reported by muon_polar_query().  The padding rows and
+ * columns of A and P are written as exact zeros by the kernels, so no caller
+ * memset is needed.
+ *
+ * All functions are asynchronous on the given HIP stream (launch only, no
+ * synchronisation) unless MUON_POLAR_DEBUG_SYNC is set in the environment, in
+ * which case every stage synchronises the stream and reports kernel faults.
+ * Pointers are device pointers.  No function allocates device memory.
+ *
+ * Numerics: fp32 accumulation on bf16 MFMA; A and P stored as bf16 (RNE of the
+ * fp32 result, P = bf16(b·A + c·(A·A)_fp32) with b, c in fp32); Y = bf16(a·X +
+ * (P·X)_fp32) with one rounding and a kept in fp32.
+ *
+ * Return value: MUON_POLAR_OK (0) or a negative status code; the thread-local
+ * message from muon_polar_last_error() gives the detail.
+ */
+#ifndef MUON_POLAR_H_
+#define MUON_POLAR_H_
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum muon_polar_status {
+    MUON_POLAR_OK = 0,
+    MUON_POLAR_ERR_INVALID_ARGUMENT = -1, /* bad shape, null pointer, m > n, ... */
+    MUON_POLAR_ERR_WORKSPACE = -2,        /* workspace missing or too small */
+    MUON_POLAR_ERR_HIP = -3,              /* a HIP runtime call or a launch failed */
+    MUON_POLAR_ERR_CONFIG = -4            /* an MUON_POLAR_* tuning variable is out of range */
+};
+
+/* Sizes of the scratch buffers for one call.
+ * Replaces the host-side tiling/launch-state builders of the reference
+ * (csrc/muon_polar_step_binding.cpp:266-611): the launch configuration is
+ * chosen and cached inside the library; the caller only needs the sizes. */
+typedef struct muon_polar_shape_info {
+    int64_t padded_rows;    /* extent and leading dimension of A and P (>= m) */
+    size_t gram_bytes;      /* bytes of one [batch, padded_rows, padded_rows] bf16 buffer */
+    size_t workspace_bytes; /* bytes for A and P together, each 256-byte aligned */
+} muon_polar_shape_info;
+
+int muon_polar_query(int64_t batch, int64_t m, int64_t n, muon_polar_shape_info *info);
+
+/* Whole step: Y = a·X + (b·A + c·A²)·X with A = X·Xᵀ, three kernels in order
+ * on `stream`.  `workspace` must hold info.workspace_bytes.
+ * Replaces MuonPolarStepAscend950 (csrc/muon_polar_step_binding.cpp:613-673)
+ * without its pad/crop copies: edges are masked in the kernels. */
+int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_bytes,
+                    int64_t batch, int64_t m, int64_t n,
+                    double a, double b, double c, hipStream_t stream);
+
+/* Stage 1: gram[bt] = X[bt]·X[bt]ᵀ into a [batch, padded_rows, padded_rows]
+ * bf16 buffer (padding written as zeros).
+ * Replaces launch_muon_gram_lowlevel_fused (csrc/muon_polar_step_binding.cpp:65-66,
+ * csrc/muon_polar_unified_ascend950.asc:512-517). */
+int muon_polar_gram(const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
+                    hipStream_t stream);
+
+/* Stage 2: poly = b·gram + c·gram·gram over [batch, padded_rows, padded_rows];
+ * gram must be symmetric (as written by stage 1).
+ * Replaces launch_muon_cube2_p_fused (csrc/muon_polar_step_binding.cpp:69-70,
+ * csrc/muon_polar_unified_ascend950.asc:1030-1035). */
+int muon_polar_poly(const void *gram, void *poly, int64_t batch, int64_t m, int64_t n,
+                    double b, double c, hipStream_t stream);
+
+/* Stage 3: Y = a·X + poly·X.
+ * Replaces launch_muon_cube3_fused_lowlevel (csrc/muon_polar_step_binding.cpp:67-68,
+ * csrc/muon_polar_unified_ascend950.asc:1535-1540). */
+int muon_polar_apply(const void *poly, const void *x, void *y, int64_t batch, int64_t m,
+                     int64_t n, double a, hipStream_t stream);
+
+/* Detail of the last failure on the calling thread ("" if none).
+ * Replaces CheckAcl / aclGetRecentErrMsg (csrc/muon_polar_step_binding.cpp:72-75). */
+const char *muon_polar_last_error(void);
+
+/* Library version string ("0.1.1" mirrors muon_ascend950/__init__.py:10). */
+const char *muon_polar_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MUON_POLAR_H_ */

@@ -1,0 +1,145 @@
+"""ctypes binding of the C ABI declared in ``include/muon_polar.h``.
+
+The torch operator (``_C.so``) links the same ``libmuon_polar.so``, so calls made
+here and through ``torch.ops.muon_ascend950.polar_step`` share one launch-config
+cache.  The tensor helpers take torch device tensors only for their pointers and
+launch on torch's current HIP stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+EXPORTED_FUNCTIONS = (
+    "muon_polar_query",
+    "muon_polar_step",
+    "muon_polar_gram",
+    "muon_polar_poly",
+    "muon_polar_apply",
+    "muon_polar_last_error",
+    "muon_polar_version",
+)
+
+OK = 0
+ERR_INVALID_ARGUMENT = -1
+ERR_WORKSPACE = -2
+ERR_HIP = -3
+ERR_CONFIG = -4
+
+
+class ShapeInfo(ctypes.Structure):
+    _fields_ = [
+        ("padded_rows", ctypes.c_int64),
+        ("gram_bytes", ctypes.c_size_t),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class CapiError(RuntimeError):
+    def __init__(self, func: str, status: int, detail: str):
+        super().__init__(f"{func} failed with status {status}: {detail}")
+        self.status = status
+        self.detail = detail
+
+
+_LIB = None
+
+
+def library_path() -> Path:
+    configured = os.environ.get("MUON_POLAR_CAPI_LIBRARY")
+    if configured:
+        return Path(configured).expanduser().resolve()
+    return Path(__file__).resolve().parent / "libmuon_polar.so"
+
+
+def load() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = library_path()
+    if not path.is_file():
+        raise RuntimeError(
+            f"libmuon_polar.so is missing at {path}; build it with "
+            "`python setup.py build_ext --inplace`"
+        )
+    lib = ctypes.CDLL(str(path))
+    i64, vp, sz, dbl = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_double
+    lib.muon_polar_query.argtypes = [i64, i64, i64, ctypes.POINTER(ShapeInfo)]
+    lib.muon_polar_step.argtypes = [vp, vp, vp, sz, i64, i64, i64, dbl, dbl, dbl, vp]
+    lib.muon_polar_gram.argtypes = [vp, vp, i64, i64, i64, vp]
+    lib.muon_polar_poly.argtypes = [vp, vp, i64, i64, i64, dbl, dbl, vp]
+    lib.muon_polar_apply.argtypes = [vp, vp, vp, i64, i64, i64, dbl, vp]
+    for name in ("muon_polar_query", "muon_polar_step", "muon_polar_gram", "muon_polar_poly",
+                 "muon_polar_apply"):
+        getattr(lib, name).restype = ctypes.c_int
+    lib.muon_polar_last_error.argtypes = []
+    lib.muon_polar_last_error.restype = ctypes.c_char_p
+    lib.muon_polar_version.argtypes = []
+    lib.muon_polar_version.restype = ctypes.c_char_p
+    _LIB = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().muon_polar_last_error().decode()
+
+
+def check(func: str, status: int) -> None:
+    if status != OK:
+        raise CapiError(func, status, last_error())
+
+
+def query(batch: int, m: int, n: int) -> ShapeInfo:
+    info = ShapeInfo()
+    check("muon_polar_query", load().muon_polar_query(batch, m, n, ctypes.byref(info)))
+    return info
+
+
+# --------------------------------------------------------------- torch tensor helpers
+def _stream(stream):
+    if stream is not None:
+        return stream
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _bmn(x):
+    if x.ndim == 2:
+        return 1, x.shape[0], x.shape[1]
+    return x.shape[0], x.shape[1], x.shape[2]
+
+
+def alloc_workspace(batch: int, m: int, n: int, device="cuda"):
+    import torch
+
+    info = query(batch, m, n)
+    return torch.empty(info.workspace_bytes, dtype=torch.uint8, device=device), info
+
+
+def step(x, y, workspace, a: float, b: float, c: float, stream=None) -> None:
+    batch, m, n = _bmn(x)
+    check("muon_polar_step", load().muon_polar_step(
+        x.data_ptr(), y.data_ptr(), workspace.data_ptr(), workspace.numel(),
+        batch, m, n, float(a), float(b), float(c), _stream(stream)))
+
+
+def gram(x, gram_buf, stream=None) -> None:
+    batch, m, n = _bmn(x)
+    check("muon_polar_gram", load().muon_polar_gram(
+        x.data_ptr(), gram_buf.data_ptr(), batch, m, n, _stream(stream)))
+
+
+def poly(gram_buf, poly_buf, batch: int, m: int, n: int, b: float, c: float, stream=None) -> None:
+    check("muon_polar_poly", load().muon_polar_poly(
+        gram_buf.data_ptr(), poly_buf.data_ptr(), batch, m, n, float(b), float(c),
+        _stream(stream)))
+
+
+def apply(poly_buf, x, y, a: float, stream=None) -> None:
+    batch, m, n = _bmn(x)
+    check("muon_polar_apply", load().muon_polar_apply(
+        poly_buf.data_ptr(), x.data_ptr(), y.data_ptr(), batch, m, n, float(a),
+        _stream(stream)))

@@ -1,0 +1,55 @@
+// muon_polar_step_binding.cpp — registers muon_ascend950::polar_step for ROCm
+// devices and forwards to the C ABI (include/muon_polar.h).
+//
+// Reference counterpart: csrc/muon_polar_step_binding.cpp:613-685.  Same schema,
+// same preconditions and error texts; differences by design:
+//   * dispatch key CUDA (how PyTorch-ROCm names HIP devices) instead of PrivateUse1;
+//   * no zero-padded input copy and no output crop (binding.cpp:630-640, 667-672):
+//     the kernels mask edge tiles, so the output is allocated at the input shape;
+//   * A and P come from one caching-allocator workspace tensor (binding.cpp:646,657);
+//   * the launch-configuration cache lives in the C ABI library.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "muon_polar.h"
+
+namespace {
+
+at::Tensor MuonPolarStepHip(const at::Tensor &x, double a, double b, double c) {
+    TORCH_CHECK(x.defined(), "muon_polar_step: x must be defined");
+    TORCH_CHECK(x.device().is_cuda(), "muon_polar_step: x must be a ROCm (HIP) device tensor");
+    TORCH_CHECK(x.scalar_type() == at::kBFloat16, "muon_polar_step: only bfloat16 is supported");
+    TORCH_CHECK(x.dim() == 3, "muon_polar_step: x must have shape [batch, M, N]");
+    TORCH_CHECK(x.size(0) > 0 && x.size(1) > 0 && x.size(2) > 0,
+                "muon_polar_step: all dimensions must be positive");
+    TORCH_CHECK(x.size(1) <= x.size(2),
+                "muon_polar_step: current prototype expects M <= N; transpose policy stays "
+                "outside this op");
+    const c10::OptionalDeviceGuard device_guard(x.device());
+    const at::Tensor input = x.contiguous();
+    const int64_t batch = input.size(0), m = input.size(1), n = input.size(2);
+
+    muon_polar_shape_info info{};
+    int st = muon_polar_query(batch, m, n, &info);
+    TORCH_CHECK(st == MUON_POLAR_OK, "muon_polar_step: ", muon_polar_last_error());
+
+    at::Tensor workspace =
+        at::empty({static_cast<int64_t>(info.workspace_bytes)}, input.options().dtype(at::kByte));
+    at::Tensor out =
+        at::empty_like(input, input.options().memory_format(c10::MemoryFormat::Contiguous));
+    hipStream_t stream = c10::hip::getCurrentHIPStream(x.device().index()).stream();
+    st = muon_polar_step(input.data_ptr(), out.data_ptr(), workspace.data_ptr(),
+                         info.workspace_bytes, batch, m, n, a, b, c, stream);
+    TORCH_CHECK(st == MUON_POLAR_OK, "muon_polar_step: ", muon_polar_last_error());
+    return out;
+}
+
+}  // namespace
+
+TORCH_LIBRARY(muon_ascend950, m) {
+    m.def("polar_step(Tensor x, float a, float b, float c) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(muon_ascend950, CUDA, m) { m.impl("polar_step", &MuonPolarStepHip); }

@@ -1,0 +1,339 @@
+// polar_capi.cpp — C ABI (include/muon_polar.h) over the gfx950 stage kernels,
+// with the launch-configuration cache.
+//
+// Reference counterpart: csrc/muon_polar_step_binding.cpp.  The reference builds
+// a CANN tiling struct per stage, copies it to device memory once per cache key
+// (binding.cpp:266-611) and keys three mutex-guarded maps by (device, stream,
+// shape, tuning knobs, coefficient bits).  Here a launch configuration is a small
+// host struct passed to the kernels by value, so one map keyed by (device, shape,
+// tuning knobs) suffices; coefficients are kernel arguments, not key material,
+// and the stream is not part of the key because nothing device-side is cached.
+#include "muon_polar.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "polar_kernels.h"
+
+namespace {
+
+using muon_polar::GemmArgs;
+using muon_polar::Stage;
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+// Same parsing rule as the reference's EnvU64 (binding.cpp:77-86): unset or
+// empty -> default; otherwise the leading decimal digits, or the default when
+// there are none.
+uint64_t env_u64(const char *name, uint64_t def, bool *present = nullptr) {
+    const char *v = std::getenv(name);
+    if (present) *present = (v != nullptr && v[0] != '\0');
+    if (v == nullptr || v[0] == '\0') return def;
+    char *end = nullptr;
+    const unsigned long long parsed = std::strtoull(v, &end, 10);
+    return end != v ? static_cast<uint64_t>(parsed) : def;
+}
+
+int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+size_t align256(size_t v) { return (v + 255u) & ~size_t(255u); }
+
+struct Knobs {
+    uint32_t gram_tile, poly_tile, apply_bm, apply_bn;
+    bool operator==(const Knobs &o) const {
+        return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
+               apply_bn == o.apply_bn;
+    }
+};
+
+struct PlanKey {
+    int device;
+    int64_t batch, m, n;
+    Knobs knobs;
+    bool operator==(const PlanKey &o) const {
+        return device == o.device && batch == o.batch && m == o.m && n == o.n && knobs == o.knobs;
+    }
+};
+
+struct PlanKeyHash {
+    size_t operator()(const PlanKey &k) const {
+        uint64_t h = 1469598103934665603ull;  // FNV-1a over the key words
+        auto mix = [&h](uint64_t v) {
+            h ^= v;
+            h *= 1099511628211ull;
+        };
+        mix(static_cast<uint64_t>(k.device));
+        mix(static_cast<uint64_t>(k.batch));
+        mix(static_cast<uint64_t>(k.m));
+        mix(static_cast<uint64_t>(k.n));
+        mix(k.knobs.gram_tile);
+        mix(k.knobs.poly_tile);
+        mix(static_cast<uint64_t>(k.knobs.apply_bm) << 32 | k.knobs.apply_bn);
+        return static_cast<size_t>(h);
+    }
+};
+
+struct Plan {
+    int64_t mp;  // padded extent / leading dimension of A and P
+    int gram_tile, poly_tile, apply_bm, apply_bn;
+    int gram_nt, poly_nt;           // tiles per side of the triangular stages
+    int apply_tm, apply_tn;         // tiles along rows / cols of stage 3
+    int64_t gram_grid, poly_grid, apply_grid;
+    size_t gram_bytes, workspace_bytes;
+};
+
+std::mutex g_plan_mutex;
+std::unordered_map<PlanKey, Plan, PlanKeyHash> g_plans;
+
+// Default tile shape by matrix size: large tiles keep the MFMA pipes fed
+// (LDS traffic per flop falls with the tile edge); small matrices need smaller
+// tiles to put enough workgroups on the 256 CUs.
+uint32_t default_square_tile(int64_t m) {
+    if (m >= 2048) return 256;
+    if (m > 256) return 128;
+    return 64;
+}
+
+int read_knobs(int64_t m, int64_t n, Knobs &k) {
+    (void)n;
+    const uint32_t def = default_square_tile(m);
+    k.gram_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_TILE", def));
+    k.poly_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_POLY_TILE", k.gram_tile));
+    k.apply_bm = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_M", def));
+    k.apply_bn = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_N", k.apply_bm));
+    if (!muon_polar::tile_supported(Stage::Gram, k.gram_tile, k.gram_tile))
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE must be 64, 128 or 256");
+    if (!muon_polar::tile_supported(Stage::Poly, k.poly_tile, k.poly_tile))
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_POLY_TILE must be 64, 128 or 256");
+    if (!muon_polar::tile_supported(Stage::Apply, k.apply_bm, k.apply_bn))
+        return fail(MUON_POLAR_ERR_CONFIG,
+                    "MUON_POLAR_APPLY_TILE_M/_N must be 64x64, 128x128, 256x256, 128x256 or "
+                    "256x128");
+    return MUON_POLAR_OK;
+}
+
+int check_shape(int64_t batch, int64_t m, int64_t n) {
+    if (batch <= 0 || m <= 0 || n <= 0)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "all dimensions must be positive");
+    if (m > n)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
+                    "expects M <= N; the transpose policy stays outside this op");
+    // 32-bit element offsets inside one matrix (X and the padded A/P).
+    if (m * n >= (int64_t(1) << 31) || round_up(m, 256) * round_up(m, 256) >= (int64_t(1) << 31))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "matrix too large (2^31 elements or more)");
+    if (batch > (int64_t(1) << 20))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "batch too large");
+    return MUON_POLAR_OK;
+}
+
+int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
+    int st = check_shape(batch, m, n);
+    if (st != MUON_POLAR_OK) return st;
+    Knobs knobs{};
+    st = read_knobs(m, n, knobs);
+    if (st != MUON_POLAR_OK) return st;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) device = -1;
+    const PlanKey key{device, batch, m, n, knobs};
+    std::lock_guard<std::mutex> lock(g_plan_mutex);
+    const auto found = g_plans.find(key);
+    if (found != g_plans.end()) {
+        out = found->second;
+        return MUON_POLAR_OK;
+    }
+    Plan p{};
+    p.gram_tile = static_cast<int>(knobs.gram_tile);
+    p.poly_tile = static_cast<int>(knobs.poly_tile);
+    p.apply_bm = static_cast<int>(knobs.apply_bm);
+    p.apply_bn = static_cast<int>(knobs.apply_bn);
+    p.mp = round_up(m, std::max(p.gram_tile, p.poly_tile));
+    p.gram_nt = static_cast<int>(p.mp / p.gram_tile);
+    p.poly_nt = static_cast<int>(p.mp / p.poly_tile);
+    p.apply_tm = static_cast<int>((m + p.apply_bm - 1) / p.apply_bm);
+    p.apply_tn = static_cast<int>((n + p.apply_bn - 1) / p.apply_bn);
+    p.gram_grid = batch * (int64_t(p.gram_nt) * (p.gram_nt + 1) / 2);
+    p.poly_grid = batch * (int64_t(p.poly_nt) * (p.poly_nt + 1) / 2);
+    p.apply_grid = batch * int64_t(p.apply_tm) * p.apply_tn;
+    p.gram_bytes = static_cast<size_t>(batch) * p.mp * p.mp * 2u;
+    p.workspace_bytes = 2 * align256(p.gram_bytes);
+    if (p.gram_grid >= (int64_t(1) << 31) || p.apply_grid >= (int64_t(1) << 31))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "grid too large");
+    g_plans.emplace(key, p);
+    out = p;
+    return MUON_POLAR_OK;
+}
+
+// MUON_POLAR_DEBUG_SYNC: synchronise after each stage when the variable is
+// present, whatever its value (reference binding.cpp:93-101; README.md:224).
+int finish_stage(hipError_t launch, hipStream_t stream, const char *stage) {
+    if (launch != hipSuccess)
+        return fail(MUON_POLAR_ERR_HIP, std::string("stage ") + stage +
+                                            " launch failed: " + hipGetErrorString(launch));
+    if (std::getenv("MUON_POLAR_DEBUG_SYNC") != nullptr) {
+        const hipError_t e = hipStreamSynchronize(stream);
+        if (e != hipSuccess)
+            return fail(MUON_POLAR_ERR_HIP,
+                        std::string("stage ") + stage + " failed: " + hipGetErrorString(e));
+    }
+    return MUON_POLAR_OK;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int run_gram(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
+             hipStream_t stream) {
+    GemmArgs g{};
+    g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(x);
+    g.out = static_cast<uint16_t *>(gram);
+    g.sb_row = g.sb_col = g.sb_epi = m * n;
+    g.sb_out = p.mp * p.mp;
+    g.ld_row = g.ld_col = g.ld_epi = static_cast<int32_t>(n);
+    g.ld_out = static_cast<int32_t>(p.mp);
+    g.row_rows = g.col_rows = static_cast<int32_t>(m);
+    g.row_k = g.col_k = static_cast<int32_t>(n);
+    g.k_loop = static_cast<int32_t>(round_up(n, 64));
+    g.out_rows = g.out_cols = static_cast<int32_t>(p.mp);
+    g.tiles_m = g.tiles_n = p.gram_nt;
+    g.tiles_per_batch = p.gram_nt * (p.gram_nt + 1) / 2;
+    g.s_epi = 0.0f;
+    g.s_acc = 1.0f;
+    (void)batch;
+    const bool vec = (n % 8 == 0) && aligned16(x);
+    return finish_stage(muon_polar::launch_gemm(Stage::Gram, p.gram_tile, p.gram_tile, vec, g,
+                                                static_cast<int>(p.gram_grid), stream),
+                        stream, "gram");
+}
+
+int run_poly(const Plan &p, const void *gram, void *poly, double b, double c,
+             hipStream_t stream) {
+    GemmArgs g{};
+    g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(gram);
+    g.out = static_cast<uint16_t *>(poly);
+    g.sb_row = g.sb_col = g.sb_epi = g.sb_out = p.mp * p.mp;
+    g.ld_row = g.ld_col = g.ld_epi = g.ld_out = static_cast<int32_t>(p.mp);
+    g.row_rows = g.col_rows = g.row_k = g.col_k = static_cast<int32_t>(p.mp);
+    g.k_loop = static_cast<int32_t>(p.mp);
+    g.out_rows = g.out_cols = static_cast<int32_t>(p.mp);
+    g.tiles_m = g.tiles_n = p.poly_nt;
+    g.tiles_per_batch = p.poly_nt * (p.poly_nt + 1) / 2;
+    g.s_epi = static_cast<float>(b);
+    g.s_acc = static_cast<float>(c);
+    return finish_stage(muon_polar::launch_gemm(Stage::Poly, p.poly_tile, p.poly_tile, true, g,
+                                                static_cast<int>(p.poly_grid), stream),
+                        stream, "poly");
+}
+
+int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t m, int64_t n,
+              double a, hipStream_t stream) {
+    GemmArgs g{};
+    g.rowop = static_cast<const uint16_t *>(poly);
+    g.colop = g.epi = static_cast<const uint16_t *>(x);
+    g.out = static_cast<uint16_t *>(y);
+    g.sb_row = p.mp * p.mp;
+    g.sb_col = g.sb_epi = g.sb_out = m * n;
+    g.ld_row = static_cast<int32_t>(p.mp);
+    g.ld_col = g.ld_epi = g.ld_out = static_cast<int32_t>(n);
+    g.row_rows = g.row_k = static_cast<int32_t>(p.mp);
+    g.col_rows = static_cast<int32_t>(n);
+    g.col_k = static_cast<int32_t>(m);
+    g.k_loop = static_cast<int32_t>(p.mp);
+    g.out_rows = static_cast<int32_t>(m);
+    g.out_cols = static_cast<int32_t>(n);
+    g.tiles_m = p.apply_tm;
+    g.tiles_n = p.apply_tn;
+    g.tiles_per_batch = p.apply_tm * p.apply_tn;
+    g.s_epi = static_cast<float>(a);
+    g.s_acc = 1.0f;
+    const bool vec = (n % 8 == 0) && aligned16(x) && aligned16(y);
+    return finish_stage(muon_polar::launch_gemm(Stage::Apply, p.apply_bm, p.apply_bn, vec, g,
+                                                static_cast<int>(p.apply_grid), stream),
+                        stream, "apply");
+}
+
+}  // namespace
+
+extern "C" {
+
+int muon_polar_query(int64_t batch, int64_t m, int64_t n, muon_polar_shape_info *info) {
+    if (info == nullptr) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "info is null");
+    Plan p{};
+    const int st = get_plan(batch, m, n, p);
+    if (st != MUON_POLAR_OK) return st;
+    info->padded_rows = p.mp;
+    info->gram_bytes = p.gram_bytes;
+    info->workspace_bytes = p.workspace_bytes;
+    return MUON_POLAR_OK;
+}
+
+int muon_polar_gram(const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
+                    hipStream_t stream) {
+    if (x == nullptr || gram == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    Plan p{};
+    const int st = get_plan(batch, m, n, p);
+    if (st != MUON_POLAR_OK) return st;
+    if (!aligned16(gram)) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram must be 16-byte aligned");
+    return run_gram(p, x, gram, batch, m, n, stream);
+}
+
+int muon_polar_poly(const void *gram, void *poly, int64_t batch, int64_t m, int64_t n, double b,
+                    double c, hipStream_t stream) {
+    if (gram == nullptr || poly == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    Plan p{};
+    const int st = get_plan(batch, m, n, p);
+    if (st != MUON_POLAR_OK) return st;
+    if (!aligned16(gram) || !aligned16(poly))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram and poly must be 16-byte aligned");
+    return run_poly(p, gram, poly, b, c, stream);
+}
+
+int muon_polar_apply(const void *poly, const void *x, void *y, int64_t batch, int64_t m, int64_t n,
+                     double a, hipStream_t stream) {
+    if (poly == nullptr || x == nullptr || y == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    Plan p{};
+    const int st = get_plan(batch, m, n, p);
+    if (st != MUON_POLAR_OK) return st;
+    if (!aligned16(poly)) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "poly must be 16-byte aligned");
+    return run_apply(p, poly, x, y, m, n, a, stream);
+}
+
+int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_bytes, int64_t batch,
+                    int64_t m, int64_t n, double a, double b, double c, hipStream_t stream) {
+    if (x == nullptr || y == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    Plan p{};
+    int st = get_plan(batch, m, n, p);
+    if (st != MUON_POLAR_OK) return st;
+    if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
+        return fail(MUON_POLAR_ERR_WORKSPACE,
+                    "workspace must hold " + std::to_string(p.workspace_bytes) + " bytes, got " +
+                        std::to_string(workspace_bytes));
+    if (!aligned16(workspace))
+        return fail(MUON_POLAR_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+    void *gram = workspace;
+    void *poly = static_cast<char *>(workspace) + align256(p.gram_bytes);
+    st = run_gram(p, x, gram, batch, m, n, stream);
+    if (st != MUON_POLAR_OK) return st;
+    st = run_poly(p, gram, poly, b, c, stream);
+    if (st != MUON_POLAR_OK) return st;
+    return run_apply(p, poly, x, y, m, n, a, stream);
+}
+
+const char *muon_polar_last_error(void) { return g_last_error.c_str(); }
+
+const char *muon_polar_version(void) { return "0.1.1"; }
+
+}  // extern "C"

@@ -1,0 +1,36 @@
+// polar_kernels.h — host-visible interface of the gfx950 stage kernels
+// (internal to the library; the public C ABI is include/muon_polar.h).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <cstdint>
+
+namespace muon_polar {
+
+enum class Stage : int { Gram = 0, Poly = 1, Apply = 2 };
+
+// Kernel arguments, passed by value (no device-side tiling buffer).
+// Element offsets inside one batch matrix are 32-bit (the host rejects matrices
+// of 2^31 elements or more); batch offsets are 64-bit.
+struct GemmArgs {
+    const uint16_t *rowop;  // K-contiguous operand whose rows index output rows
+    const uint16_t *colop;  // gram/poly: K-contiguous, rows index output cols;
+                            // apply: [K][cols] N-contiguous (X)
+    const uint16_t *epi;    // epilogue input: A (poly) or X (apply); unused by gram
+    uint16_t *out;
+    int64_t sb_row, sb_col, sb_epi, sb_out;  // batch strides in elements
+    int32_t ld_row, ld_col, ld_epi, ld_out;  // leading dimensions in elements
+    int32_t row_rows, row_k;                 // extents of rowop present in memory
+    int32_t col_rows, col_k;                 // gram/poly: rows x K of colop; apply: cols x K
+    int32_t k_loop;                          // K extent iterated (multiple of 64)
+    int32_t out_rows, out_cols;              // store extent (apply only)
+    int32_t tiles_m, tiles_n, tiles_per_batch;
+    float s_epi, s_acc;  // poly: b, c;  apply: a, 1
+};
+
+bool tile_supported(Stage s, int bm, int bn);
+
+hipError_t launch_gemm(Stage s, int bm, int bn, bool vec, const GemmArgs &g, int grid,
+                       hipStream_t stream);
+
+}  // namespace muon_polar

@@ -1,0 +1,224 @@
+"""CPU oracle for one Polar Express step — TEST INFRASTRUCTURE ONLY.
+
+This module restates the reference's algorithm on the CPU so that tests can
+check the HIP path against it.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker
+or the reported CPU baseline; the product path (``muon_fusion_ascend950_amd``)
+never calls it and has no CPU fallback.
+
+What it restates (reference file:line):
+
+* ``reference_formula`` — the reference's own oracle, ``tests/test_polar_step.py:22-28``:
+  ``gram = x @ x.mT; polynomial = b*gram + c*(gram@gram); out = a*out + polynomial@out``,
+  looped over coefficient triples.  ``reference_formula_torch`` runs it in torch with the
+  caller's dtype (bf16 like the reference test, or fp32); ``polar_step_f64`` runs one step
+  in float64 numpy.
+* ``make_input`` — the input recipe of ``tests/test_polar_step.py:38-39`` (bf16 N(0,1),
+  divided per matrix by ``‖x‖_F·1.01 + 1e-6``) with a seeded CPU generator.
+* ``polar_step_fused`` — the rounding points the kernels implement, which follow the
+  reference kernels' storage choices (``csrc/muon_polar_step_binding.cpp:641-664``: A and P
+  are bf16 tensors; ``.asc:407`` RNE cast of A; ``.asc:929-940`` P = RNE(b·A + c·A²) in
+  fp32) and, for Y, one rounding of ``a·X + P·X`` (the reference instead rounds P·X, a·X and
+  the sum separately in bf16, ``.asc:1472-1476``).  Products are summed exactly (float64),
+  so it differs from a kernel only by the kernel's fp32 accumulation error.
+* ``bf16_round`` / ``f32_to_bf16_bits`` — round-to-nearest-even from the IEEE definition,
+  as ``FloatToBf16Bits`` (``csrc/muon_polar_step_binding.cpp:156-162``), plus NaN/inf
+  handling.
+* ``pad_crop_step`` — the reference binding's pad-to-128/16 + crop semantics
+  (``csrc/muon_polar_step_binding.cpp:630-672``), to show masking equals padding.
+* ``wrapper_step`` — the Python wrapper's M > N transpose policy (``muon_ascend950/ops.py:24-33``).
+
+How each function is pinned (``tests/test_oracle.py``): SVD closed form (one step maps
+singular values σ -> aσ + bσ³ + cσ⁵, five steps compose), textbook special cases of each
+stage, brute-force loops on tiny inputs, bf16 rounding against torch's RNE conversion, and
+planted mistakes that must fail those checks.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+# tests/test_polar_step.py:13-19 (= examples/five_steps.py:7-13 = README.md:101-107)
+COEFFICIENTS = (
+    (8.156554524902461, -22.48329292557795, 15.878769915207462),
+    (4.042929935166739, -2.808917465908714, 0.5000178451051316),
+    (3.8916678022926607, -2.772484153217685, 0.5060648178503393),
+    (3.285753657755655, -2.3681294933425376, 0.46449024233003106),
+    (2.3465413258596377, -1.7097828382687081, 0.42323551169305323),
+)
+
+
+# ----------------------------------------------------------------------------- bf16
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """Round float32 values to bf16 (nearest, ties to even); returns uint16 bit patterns.
+
+    binding.cpp:156-162 adds 0x7FFF + lsb to the raw bits; NaNs are kept quiet NaNs
+    (a plain add could carry a NaN payload into infinity).
+    """
+    f = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = f.view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    rounded = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
+    nan = np.isnan(f)
+    if np.any(nan):
+        rounded = np.where(nan, ((u >> 16).astype(np.uint16) | np.uint16(0x0040)), rounded)
+    return rounded.astype(np.uint16)
+
+
+def bf16_bits_to_f32(bits) -> np.ndarray:
+    b = np.ascontiguousarray(np.asarray(bits, dtype=np.uint16))
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_round(x) -> np.ndarray:
+    """Value of x (any float dtype) after float32 then bf16 RNE rounding, as float32."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(x, dtype=np.float32)))
+
+
+# ----------------------------------------------------------------------------- inputs
+def make_input(shape, seed: int = 0):
+    """bf16 torch CPU tensor per tests/test_polar_step.py:38-39, seeded.
+
+    randn in bf16 from a CPU generator, then x / (‖x‖_F(last two dims)·1.01 + 1e-6),
+    evaluated in bf16 on the CPU so every box gets the same bits.
+    """
+    import torch
+
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(shape, dtype=torch.bfloat16, generator=gen)
+    return x / (x.norm(dim=(-2, -1), keepdim=True) * 1.01 + 1e-6)
+
+
+def to_numpy_f64(t) -> np.ndarray:
+    return t.detach().to("cpu").float().numpy().astype(np.float64)
+
+
+# ----------------------------------------------------------------------------- formula
+def _mT(x: np.ndarray) -> np.ndarray:
+    return np.swapaxes(x, -1, -2)
+
+
+def gram_f64(x: np.ndarray) -> np.ndarray:
+    """A = X·Xᵀ (tests/test_polar_step.py:25)."""
+    x = np.asarray(x, dtype=np.float64)
+    return x @ _mT(x)
+
+
+def poly_f64(gram: np.ndarray, b: float, c: float) -> np.ndarray:
+    """P = b·A + c·A·A (tests/test_polar_step.py:26)."""
+    g = np.asarray(gram, dtype=np.float64)
+    return b * g + c * (g @ g)
+
+
+def apply_f64(poly: np.ndarray, x: np.ndarray, a: float) -> np.ndarray:
+    """Y = a·X + P·X (tests/test_polar_step.py:27)."""
+    x = np.asarray(x, dtype=np.float64)
+    return a * x + np.asarray(poly, dtype=np.float64) @ x
+
+
+def polar_step_f64(x: np.ndarray, a: float, b: float, c: float) -> np.ndarray:
+    """One step in float64 (the formula of tests/test_polar_step.py:22-28)."""
+    return apply_f64(poly_f64(gram_f64(x), b, c), x, a)
+
+
+def reference_formula_f64(x: np.ndarray, coefficients) -> np.ndarray:
+    out = np.asarray(x, dtype=np.float64)
+    for a, b, c in coefficients:
+        out = polar_step_f64(out, a, b, c)
+    return out
+
+
+def reference_formula_torch(x, coefficients):
+    """tests/test_polar_step.py:22-28, in x's dtype and on x's device.
+
+    The transposed operand is materialised (``.contiguous()``) before the product:
+    same values, but batched bf16 products with a transposed right operand have
+    faulted ROCm GPUs, so no such call is made.
+    """
+    import torch
+
+    out = x
+    for a, b, c in coefficients:
+        gram = torch.matmul(out, out.mT.contiguous())
+        polynomial = b * gram + c * torch.matmul(gram, gram)
+        out = a * out + torch.matmul(polynomial, out)
+    return out
+
+
+# ----------------------------------------------------------------------------- kernel rounding points
+def polar_step_fused(x: np.ndarray, a: float, b: float, c: float, return_stages: bool = False):
+    """One step with the kernels' rounding points, exact sums.
+
+    A = bf16(X·Xᵀ); P = bf16(b·A + c·(A·A)) with b, c as fp32; Y = bf16(a·X + P·X) with
+    a as fp32.  X must hold bf16 values.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    a32, b32, c32 = (float(np.float32(v)) for v in (a, b, c))
+    gram = bf16_round(gram_f64(x)).astype(np.float64)
+    poly = bf16_round(b32 * gram + c32 * (gram @ gram)).astype(np.float64)
+    y = bf16_round(a32 * x + poly @ x).astype(np.float64)
+    if return_stages:
+        return y, gram, poly
+    return y
+
+
+def five_step_fused(x: np.ndarray, coefficients=COEFFICIENTS) -> np.ndarray:
+    out = np.asarray(x, dtype=np.float64)
+    for a, b, c in coefficients:
+        out = polar_step_fused(out, a, b, c)
+    return out
+
+
+# ----------------------------------------------------------------------------- boundary semantics
+def pad_crop_step(x: np.ndarray, a: float, b: float, c: float, step=polar_step_fused):
+    """Reference binding semantics (binding.cpp:630-672): zero-pad rows to a multiple of
+    128 and columns to max(multiple of 16, padded rows), run, crop."""
+    x = np.asarray(x, dtype=np.float64)
+    *lead, m, n = x.shape
+    rows = -(-m // 128) * 128
+    cols = max(-(-n // 16) * 16, rows)
+    padded = np.zeros((*lead, rows, cols), dtype=np.float64)
+    padded[..., :m, :n] = x
+    return step(padded, a, b, c)[..., :m, :n]
+
+
+def wrapper_step(x: np.ndarray, a: float, b: float, c: float, step=polar_step_fused):
+    """ops.py:24-33: [M,N] -> [1,M,N]; transpose when M > N; undo both afterwards."""
+    x = np.asarray(x, dtype=np.float64)
+    squeeze = x.ndim == 2
+    work = x[None] if squeeze else x
+    transposed = work.shape[-2] > work.shape[-1]
+    if transposed:
+        work = _mT(work)
+    out = step(work, a, b, c)
+    if transposed:
+        out = _mT(out)
+    return out[0] if squeeze else out
+
+
+# ----------------------------------------------------------------------------- metrics
+def rel_frobenius(actual, expected) -> float:
+    """‖actual − expected‖_F / ‖expected‖_F over the whole tensor."""
+    actual = np.asarray(actual, dtype=np.float64)
+    expected = np.asarray(expected, dtype=np.float64)
+    den = np.linalg.norm(expected.ravel())
+    return float(np.linalg.norm((actual - expected).ravel()) / (den if den > 0 else 1.0))
+
+
+def bf16_ulp_distance(a_bits, b_bits) -> np.ndarray:
+    """Distance in bf16 units in the last place between two arrays of bf16 bit patterns."""
+
+    def ordered(bits):
+        v = np.asarray(bits, dtype=np.uint16).astype(np.int32)
+        return np.where(v & 0x8000, 0x8000 - v, v)  # monotone map of bf16 to integers
+
+    return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+def scalar_polynomial(sigma, coefficients) -> np.ndarray:
+    """Singular-value map of the steps: σ -> aσ + bσ³ + cσ⁵, composed over triples."""
+    s = np.asarray(sigma, dtype=np.float64)
+    for a, b, c in coefficients:
+        s = a * s + b * s**3 + c * s**5
+    return s
+
