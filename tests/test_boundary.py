@@ -1,0 +1,194 @@
+"""Host-side boundary: Python surface, torch op registration, FakeTensor path and the
+C ABI library — everything that runs without a GPU.
+
+Reference behaviour being mirrored: muon_ascend950/ops.py:6-33 (checks, 2-D/3-D,
+M > N transpose), _loader.py:10-49 (library discovery, fake kernel), and the op schema
+of csrc/muon_polar_step_binding.cpp:677-685.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+import muon_fusion_ascend950_amd as mf
+from muon_fusion_ascend950_amd import _loader, capi
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "muon_polar.h"
+C0 = (8.156554524902461, -22.48329292557795, 15.878769915207462)
+
+
+# ----------------------------------------------------------------------------- python surface
+def test_public_surface():
+    import muon_ascend950
+
+    assert muon_ascend950.polar_step is mf.polar_step
+    assert mf.__version__ == "0.1.1" == muon_ascend950.__version__
+    assert mf.__all__ == ["polar_step"]
+
+
+def test_rejects_non_tensor():
+    with pytest.raises(TypeError, match="torch.Tensor"):
+        mf.polar_step([[1.0]], *C0)
+
+
+def test_rejects_cpu_tensor():
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        mf.polar_step(torch.zeros(4, 8, dtype=torch.bfloat16), *C0)
+
+
+@pytest.mark.parametrize(
+    "shape,dtype,exc,msg",
+    [
+        ((4, 8), torch.float32, TypeError, "bfloat16"),
+        ((4, 8), torch.float16, TypeError, "bfloat16"),
+        ((8,), torch.bfloat16, ValueError, "shape"),
+        ((1, 2, 4, 8), torch.bfloat16, ValueError, "shape"),
+        ((0, 8), torch.bfloat16, ValueError, "positive"),
+        ((2, 0, 8), torch.bfloat16, ValueError, "positive"),
+    ],
+)
+def test_argument_checks_on_device_tensors(shape, dtype, exc, msg):
+    with FakeTensorMode():
+        x = torch.empty(shape, dtype=dtype, device="cuda")
+        with pytest.raises(exc, match=msg):
+            mf.polar_step(x, *C0)
+
+
+@pytest.mark.parametrize("shape", [(129, 130), (130, 129), (2, 150, 2050), (3, 70, 20), (1, 1)])
+def test_fake_path_preserves_shape_and_dtype(shape):
+    # FakeTensor kernel registered by the loader (reference _loader.py:41-48)
+    with FakeTensorMode():
+        x = torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+        y = mf.polar_step(x, *C0)
+        assert y.shape == x.shape and y.dtype == torch.bfloat16 and y.device == x.device
+        assert y.is_contiguous()
+
+
+def test_fake_kernel_on_op_directly():
+    with FakeTensorMode():
+        x = torch.empty(2, 5, 9, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+        y = torch.ops.muon_ascend950.polar_step(x, 1.0, 2.0, 3.0)
+        assert y.shape == x.shape and y.is_contiguous()
+
+
+def test_op_schema_matches_reference():
+    schema = str(torch.ops.muon_ascend950.polar_step.default._schema)
+    assert schema == "muon_ascend950::polar_step(Tensor x, float a, float b, float c) -> Tensor"
+
+
+def test_loader_is_idempotent():
+    _loader.load_library()
+    _loader.load_library()
+    assert _loader._LOADED
+
+
+def test_loader_env_override(monkeypatch, tmp_path):
+    monkeypatch.setenv("MUON_ASCEND950_LIBRARY", str(tmp_path / "missing.so"))
+    with pytest.raises(RuntimeError, match="does not exist"):
+        _loader._library_path()
+    real = next((ROOT / "muon_fusion_ascend950_amd").glob("_C*.so"))
+    monkeypatch.setenv("MUON_ASCEND950_LIBRARY", str(real))
+    assert _loader._library_path() == real.resolve()
+
+
+def test_import_fails_loudly_without_native_library(tmp_path):
+    """A missing native library is a hard error at import: there is no CPU fallback."""
+    pkg = tmp_path / "muon_fusion_ascend950_amd"
+    pkg.mkdir()
+    for f in ("__init__.py", "_loader.py", "ops.py"):
+        (pkg / f).write_text((ROOT / "muon_fusion_ascend950_amd" / f).read_text())
+    env = dict(os.environ, PYTHONPATH=str(tmp_path))
+    env.pop("MUON_ASCEND950_LIBRARY", None)
+    proc = subprocess.run([sys.executable, "-c", "import muon_fusion_ascend950_amd"],
+                          cwd=tmp_path, env=env, capture_output=True, text=True, timeout=300)
+    assert proc.returncode != 0
+    assert "native library is missing" in proc.stderr
+
+
+# ----------------------------------------------------------------------------- C ABI library
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(muon_polar_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_exported_set():
+    assert declared_functions() == sorted(capi.EXPORTED_FUNCTIONS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(capi.library_path()))
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(capi.library_path())],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (muon_polar_\w+)$", out, re.M))
+    assert exported == set(declared_functions())
+
+
+def test_capi_version():
+    assert capi.load().muon_polar_version().decode() == "0.1.1"
+
+
+@pytest.mark.parametrize("batch,m,n", [(1, 129, 130), (2, 150, 2050), (8, 512, 2048),
+                                       (1, 4096, 14336), (4, 4096, 4096), (3, 1, 1)])
+def test_query_sizes(batch, m, n):
+    info = capi.query(batch, m, n)
+    mp = info.padded_rows
+    assert mp >= m and mp % 64 == 0 and mp - m < 256
+    assert info.gram_bytes == batch * mp * mp * 2
+    assert info.workspace_bytes >= 2 * info.gram_bytes
+    assert info.workspace_bytes % 256 == 0
+
+
+@pytest.mark.parametrize("batch,m,n", [(0, 4, 4), (1, 0, 4), (1, 4, 0), (1, 5, 4), (-1, 4, 4)])
+def test_query_rejects_bad_shapes(batch, m, n):
+    with pytest.raises(capi.CapiError) as err:
+        capi.query(batch, m, n)
+    assert err.value.status == capi.ERR_INVALID_ARGUMENT
+
+
+def test_query_rejects_oversized_matrix():
+    with pytest.raises(capi.CapiError, match="too large"):
+        capi.query(1, 46341, 46341)
+
+
+def test_entry_points_validate_before_launch():
+    lib = capi.load()
+    assert lib.muon_polar_step(None, None, None, 0, 1, 4, 8, 1.0, 1.0, 1.0, None) == capi.ERR_INVALID_ARGUMENT
+    # non-null but never dereferenced: the workspace check fails first, nothing launches
+    assert lib.muon_polar_step(16, 16, None, 0, 1, 4, 8, 1.0, 1.0, 1.0, None) == capi.ERR_WORKSPACE
+    assert "workspace must hold" in capi.last_error()
+    assert lib.muon_polar_step(16, 16, 16, 1, 1, 4, 8, 1.0, 1.0, 1.0, None) == capi.ERR_WORKSPACE
+    assert lib.muon_polar_step(16, 16, 16, 1 << 20, 1, 8, 4, 1.0, 1.0, 1.0, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_gram(None, 16, 1, 4, 8, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_poly(16, None, 1, 4, 8, 1.0, 1.0, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_apply(16, 16, None, 1, 4, 8, 1.0, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_gram(16, 17, 1, 4, 8, None) == capi.ERR_INVALID_ARGUMENT  # misaligned
+
+
+@pytest.mark.parametrize("var,value", [("MUON_POLAR_GRAM_TILE", "96"), ("MUON_POLAR_POLY_TILE", "512"),
+                                       ("MUON_POLAR_APPLY_TILE_M", "32"),
+                                       ("MUON_POLAR_APPLY_TILE_N", "100")])
+def test_bad_tuning_variable_is_a_config_error(monkeypatch, var, value):
+    monkeypatch.setenv(var, value)
+    with pytest.raises(capi.CapiError) as err:
+        capi.query(1, 512, 2048)
+    assert err.value.status == capi.ERR_CONFIG
+
+
+def test_tuning_variables_enter_the_plan(monkeypatch):
+    monkeypatch.setenv("MUON_POLAR_GRAM_TILE", "256")
+    assert capi.query(1, 300, 700).padded_rows == 512
+    monkeypatch.setenv("MUON_POLAR_GRAM_TILE", "64")
+    monkeypatch.setenv("MUON_POLAR_POLY_TILE", "64")
+    assert capi.query(1, 300, 700).padded_rows == 320
