@@ -74,20 +74,17 @@ def _torch_paths() -> tuple[list[str], Path]:
 def build_hip_library(verbose: bool = True) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     common = HIP_FLAGS + [f"-I{INCLUDE}", f"-I{CSRC}"]
-    jobs = [
-        ([_hipcc(), "-x", "hip", "-c", str(CSRC / "polar_kernels.hip"), "-o",
-          str(BUILD_DIR / "polar_kernels.o")] + common),
-        ([_hipcc(), "-x", "hip", "-c", str(CSRC / "polar_capi.cpp"), "-o",
-          str(BUILD_DIR / "polar_capi.o")] + common),
-    ]
+    sources = ["polar_kernels.hip", "polar_stream.hip", "polar_capi.cpp"]
+    objects = [BUILD_DIR / (Path(src).stem + ".o") for src in sources]
+    jobs = [[_hipcc(), "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)] + common
+            for src, obj in zip(sources, objects)]
     with concurrent.futures.ThreadPoolExecutor(max_workers=len(jobs)) as pool:
         for fut in [pool.submit(_run, cmd, verbose) for cmd in jobs]:
             fut.result()
     out = PKG_DIR / "libmuon_polar.so"
     tmp = out.with_suffix(".so.tmp")
-    _run([_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}",
-          str(BUILD_DIR / "polar_kernels.o"), str(BUILD_DIR / "polar_capi.o"),
-          "-Wl,-soname,libmuon_polar.so", "-o", str(tmp)], verbose)
+    _run([_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}"] + [str(o) for o in objects]
+         + ["-Wl,-soname,libmuon_polar.so", "-o", str(tmp)], verbose)
     os.replace(tmp, out)
     return out
 

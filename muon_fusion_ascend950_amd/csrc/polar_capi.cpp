@@ -51,9 +51,10 @@ size_t align256(size_t v) { return (v + 255u) & ~size_t(255u); }
 
 struct Knobs {
     uint32_t gram_tile, poly_tile, apply_bm, apply_bn;
+    uint32_t stream;  // 1: DMA-fed kernels where eligible; 0: register-staged kernels only
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
-               apply_bn == o.apply_bn;
+               apply_bn == o.apply_bn && stream == o.stream;
     }
 };
 
@@ -80,6 +81,7 @@ struct PlanKeyHash {
         mix(k.knobs.gram_tile);
         mix(k.knobs.poly_tile);
         mix(static_cast<uint64_t>(k.knobs.apply_bm) << 32 | k.knobs.apply_bn);
+        mix(k.knobs.stream);
         return static_cast<size_t>(h);
     }
 };
@@ -91,6 +93,7 @@ struct Plan {
     int apply_tm, apply_tn;         // tiles along rows / cols of stage 3
     int64_t gram_grid, poly_grid, apply_grid;
     size_t gram_bytes, workspace_bytes;
+    bool stream;
 };
 
 std::mutex g_plan_mutex;
@@ -112,6 +115,8 @@ int read_knobs(int64_t m, int64_t n, Knobs &k) {
     k.poly_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_POLY_TILE", k.gram_tile));
     k.apply_bm = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_M", def));
     k.apply_bn = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_N", k.apply_bm));
+    k.stream = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM", 1));
+    if (k.stream > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM must be 0 or 1");
     if (!muon_polar::tile_supported(Stage::Gram, k.gram_tile, k.gram_tile))
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE must be 64, 128 or 256");
     if (!muon_polar::tile_supported(Stage::Poly, k.poly_tile, k.poly_tile))
@@ -129,9 +134,9 @@ int check_shape(int64_t batch, int64_t m, int64_t n) {
     if (m > n)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
                     "expects M <= N; the transpose policy stays outside this op");
-    // 32-bit element offsets inside one matrix (X and the padded A/P).
-    if (m * n >= (int64_t(1) << 31) || round_up(m, 256) * round_up(m, 256) >= (int64_t(1) << 31))
-        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "matrix too large (2^31 elements or more)");
+    // 32-bit byte offsets inside one matrix (X and the padded A/P): < 2^31 bytes.
+    if (m * n >= (int64_t(1) << 30) || round_up(m, 256) * round_up(m, 256) >= (int64_t(1) << 30))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "matrix too large (2^30 elements or more)");
     if (batch > (int64_t(1) << 20))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "batch too large");
     return MUON_POLAR_OK;
@@ -167,6 +172,7 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.apply_grid = batch * int64_t(p.apply_tm) * p.apply_tn;
     p.gram_bytes = static_cast<size_t>(batch) * p.mp * p.mp * 2u;
     p.workspace_bytes = 2 * align256(p.gram_bytes);
+    p.stream = knobs.stream != 0;
     if (p.gram_grid >= (int64_t(1) << 31) || p.apply_grid >= (int64_t(1) << 31))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "grid too large");
     g_plans.emplace(key, p);
@@ -191,6 +197,15 @@ int finish_stage(hipError_t launch, hipStream_t stream, const char *stage) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Launch one stage: DMA-fed kernel when allowed, register-staged otherwise.
+hipError_t launch_stage(Stage s, int bm, int bn, bool stream_ok, bool vec, GemmArgs &g,
+                        int64_t batch, int64_t grid, hipStream_t stream) {
+    g.total_tiles = static_cast<int32_t>(batch * g.tiles_per_batch);
+    g.per_xcd = (g.total_tiles + 7) / 8;
+    if (stream_ok) return muon_polar::launch_stream(s, bm, bn, g, stream);
+    return muon_polar::launch_gemm(s, bm, bn, vec, g, static_cast<int>(grid), stream);
+}
+
 int run_gram(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
              hipStream_t stream) {
     GemmArgs g{};
@@ -208,14 +223,14 @@ int run_gram(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m,
     g.tiles_per_batch = p.gram_nt * (p.gram_nt + 1) / 2;
     g.s_epi = 0.0f;
     g.s_acc = 1.0f;
-    (void)batch;
+    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
     const bool vec = (n % 8 == 0) && aligned16(x);
-    return finish_stage(muon_polar::launch_gemm(Stage::Gram, p.gram_tile, p.gram_tile, vec, g,
-                                                static_cast<int>(p.gram_grid), stream),
+    return finish_stage(launch_stage(Stage::Gram, p.gram_tile, p.gram_tile, p.stream && vec, vec,
+                                     g, batch, p.gram_grid, stream),
                         stream, "gram");
 }
 
-int run_poly(const Plan &p, const void *gram, void *poly, double b, double c,
+int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double b, double c,
              hipStream_t stream) {
     GemmArgs g{};
     g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(gram);
@@ -229,13 +244,14 @@ int run_poly(const Plan &p, const void *gram, void *poly, double b, double c,
     g.tiles_per_batch = p.poly_nt * (p.poly_nt + 1) / 2;
     g.s_epi = static_cast<float>(b);
     g.s_acc = static_cast<float>(c);
-    return finish_stage(muon_polar::launch_gemm(Stage::Poly, p.poly_tile, p.poly_tile, true, g,
-                                                static_cast<int>(p.poly_grid), stream),
+    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(p.mp * p.mp * 2);
+    return finish_stage(launch_stage(Stage::Poly, p.poly_tile, p.poly_tile, p.stream, true, g,
+                                     batch, p.poly_grid, stream),
                         stream, "poly");
 }
 
-int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t m, int64_t n,
-              double a, hipStream_t stream) {
+int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t batch, int64_t m,
+              int64_t n, double a, hipStream_t stream) {
     GemmArgs g{};
     g.rowop = static_cast<const uint16_t *>(poly);
     g.colop = g.epi = static_cast<const uint16_t *>(x);
@@ -255,9 +271,11 @@ int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t m
     g.tiles_per_batch = p.apply_tm * p.apply_tn;
     g.s_epi = static_cast<float>(a);
     g.s_acc = 1.0f;
+    g.bytes_row = static_cast<uint32_t>(p.mp * p.mp * 2);
+    g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
     const bool vec = (n % 8 == 0) && aligned16(x) && aligned16(y);
-    return finish_stage(muon_polar::launch_gemm(Stage::Apply, p.apply_bm, p.apply_bn, vec, g,
-                                                static_cast<int>(p.apply_grid), stream),
+    return finish_stage(launch_stage(Stage::Apply, p.apply_bm, p.apply_bn, p.stream && vec, vec,
+                                     g, batch, p.apply_grid, stream),
                         stream, "apply");
 }
 
@@ -296,7 +314,7 @@ int muon_polar_poly(const void *gram, void *poly, int64_t batch, int64_t m, int6
     if (st != MUON_POLAR_OK) return st;
     if (!aligned16(gram) || !aligned16(poly))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram and poly must be 16-byte aligned");
-    return run_poly(p, gram, poly, b, c, stream);
+    return run_poly(p, gram, poly, batch, b, c, stream);
 }
 
 int muon_polar_apply(const void *poly, const void *x, void *y, int64_t batch, int64_t m, int64_t n,
@@ -307,7 +325,7 @@ int muon_polar_apply(const void *poly, const void *x, void *y, int64_t batch, in
     const int st = get_plan(batch, m, n, p);
     if (st != MUON_POLAR_OK) return st;
     if (!aligned16(poly)) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "poly must be 16-byte aligned");
-    return run_apply(p, poly, x, y, m, n, a, stream);
+    return run_apply(p, poly, x, y, batch, m, n, a, stream);
 }
 
 int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_bytes, int64_t batch,
@@ -327,9 +345,9 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
     void *poly = static_cast<char *>(workspace) + align256(p.gram_bytes);
     st = run_gram(p, x, gram, batch, m, n, stream);
     if (st != MUON_POLAR_OK) return st;
-    st = run_poly(p, gram, poly, b, c, stream);
+    st = run_poly(p, gram, poly, batch, b, c, stream);
     if (st != MUON_POLAR_OK) return st;
-    return run_apply(p, poly, x, y, m, n, a, stream);
+    return run_apply(p, poly, x, y, batch, m, n, a, stream);
 }
 
 const char *muon_polar_last_error(void) { return g_last_error.c_str(); }

@@ -26,11 +26,20 @@ struct GemmArgs {
     int32_t out_rows, out_cols;              // store extent (apply only)
     int32_t tiles_m, tiles_n, tiles_per_batch;
     float s_epi, s_acc;  // poly: b, c;  apply: a, 1
+    // streaming kernels only
+    int32_t total_tiles, per_xcd;   // batch * tiles_per_batch; ceil(total_tiles / 8)
+    uint32_t bytes_row, bytes_col;  // byte extent of one batch matrix of rowop / colop
+    uint32_t bytes_epi;             // byte extent of one batch matrix of epi
 };
 
 bool tile_supported(Stage s, int bm, int bn);
 
+// Register-staged kernels: any shape and alignment (element-masked edges).
 hipError_t launch_gemm(Stage s, int bm, int bn, bool vec, const GemmArgs &g, int grid,
                        hipStream_t stream);
+
+// DMA-fed kernels: X chunks of 16 B must be entirely inside or outside the matrix
+// (n % 8 == 0, 16-byte aligned X).  Grid is 8 * g.per_xcd.
+hipError_t launch_stream(Stage s, int bm, int bn, const GemmArgs &g, hipStream_t stream);
 
 }  // namespace muon_polar

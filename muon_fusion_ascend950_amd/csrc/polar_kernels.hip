@@ -20,23 +20,11 @@
 // therefore exact zeros, so stages 2 and 3 need no K masking on A or P.
 #include "polar_kernels.h"
 #include "polar_tile.hpp"
+#include "polar_epilogue.hpp"
 
 namespace muon_polar {
 
 namespace {
-
-// Output tile (tm, tn) of linear tile index t within one batch matrix.
-// Triangular schedule (stages 1, 2): row-major walk over tn >= tm.
-__device__ __forceinline__ void upper_tile_of(int t, int nt, int &tm, int &tn) {
-    int row = 0, len = nt;
-    while (t >= len) {
-        t -= len;
-        ++row;
-        --len;
-    }
-    tm = row;
-    tn = row + t;
-}
 
 template <int BM, int BN, Stage S, bool VEC>
 __global__ __launch_bounds__(256) void polar_gemm_kernel(GemmArgs g) {
@@ -128,88 +116,7 @@ __global__ __launch_bounds__(256) void polar_gemm_kernel(GemmArgs g) {
     }
 
     // ---------------------------------------------------------------- epilogue
-    uint16_t *out = g.out + bt * g.sb_out;
-    const uint16_t *epi = g.epi + bt * g.sb_epi;
-    const bool diag = (S != Stage::Apply) && (tm == tn);
-#pragma unroll
-    for (int i = 0; i < SM; ++i) {
-        const int r = row0 + wr * WM + i * 32 + (lane & 31);
-#pragma unroll
-        for (int j = 0; j < SN; ++j) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int c = col0 + wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
-
-                if constexpr (S == Stage::Apply) {
-                    // Y = bf16(a·X + T), one rounding, a in fp32.
-                    if (r < g.out_rows) {
-                        const uint16_t *xr = epi + r * g.ld_epi + c;
-                        uint16_t *yr = out + r * g.ld_out + c;
-                        if (VEC && c + 3 < g.out_cols) {
-                            const u32x2 xv = *reinterpret_cast<const u32x2 *>(xr);
-                            const float x0 = bf16_bits_to_f32(xv[0] & 0xffffu);
-                            const float x1 = bf16_bits_to_f32(xv[0] >> 16);
-                            const float x2 = bf16_bits_to_f32(xv[1] & 0xffffu);
-                            const float x3 = bf16_bits_to_f32(xv[1] >> 16);
-                            const uint32_t y0 = f32_to_bf16_bits(fmaf(g.s_epi, x0, v[0]));
-                            const uint32_t y1 = f32_to_bf16_bits(fmaf(g.s_epi, x1, v[1]));
-                            const uint32_t y2 = f32_to_bf16_bits(fmaf(g.s_epi, x2, v[2]));
-                            const uint32_t y3 = f32_to_bf16_bits(fmaf(g.s_epi, x3, v[3]));
-                            *reinterpret_cast<u32x2 *>(yr) = u32x2{y0 | (y1 << 16), y2 | (y3 << 16)};
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                if (c + e < g.out_cols) {
-                                    const float x = bf16_bits_to_f32(xr[e]);
-                                    yr[e] = f32_to_bf16_bits(fmaf(g.s_epi, x, v[e]));
-                                }
-                            }
-                        }
-                    }
-                } else {
-                    uint16_t h[4];
-                    if constexpr (S == Stage::Poly) {
-                        // P = bf16(b·A + c·(A·A)), fp32 arithmetic.
-                        const u32x2 av =
-                            *reinterpret_cast<const u32x2 *>(epi + r * g.ld_epi + c);
-                        const float a0 = bf16_bits_to_f32(av[0] & 0xffffu);
-                        const float a1 = bf16_bits_to_f32(av[0] >> 16);
-                        const float a2 = bf16_bits_to_f32(av[1] & 0xffffu);
-                        const float a3 = bf16_bits_to_f32(av[1] >> 16);
-                        h[0] = f32_to_bf16_bits(fmaf(g.s_acc, v[0], g.s_epi * a0));
-                        h[1] = f32_to_bf16_bits(fmaf(g.s_acc, v[1], g.s_epi * a1));
-                        h[2] = f32_to_bf16_bits(fmaf(g.s_acc, v[2], g.s_epi * a2));
-                        h[3] = f32_to_bf16_bits(fmaf(g.s_acc, v[3], g.s_epi * a3));
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16_bits(v[e]);
-                    }
-                    uint16_t *orow = out + r * g.ld_out + c;
-                    if (!diag) {
-                        *reinterpret_cast<u32x2 *>(orow) =
-                            u32x2{uint32_t(h[0]) | (uint32_t(h[1]) << 16),
-                                  uint32_t(h[2]) | (uint32_t(h[3]) << 16)};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) out[(c + e) * g.ld_out + r] = h[e];
-                    } else {
-                        // Diagonal tile: the element with row <= col is the single
-                        // source of both (r, c) and (c, r), so A and P are bitwise
-                        // symmetric.
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            if (r <= c + e) {
-                                orow[e] = h[e];
-                                out[(c + e) * g.ld_out + r] = h[e];
-                            }
-                        }
-                    }
-                }
-            }
-        }
-    }
+    store_tile<BM, BN, S, VEC>(acc, g, bt, row0, col0, tm == tn, lane, wr, wc);
 }
 
 template <int BM, int BN, Stage S, bool VEC>

@@ -1,0 +1,381 @@
+// polar_stream.hip — DMA-fed variant of the three stage kernels.
+//
+// Same tiles, MFMA layout and arithmetic as the register-staged kernels in
+// polar_kernels.hip; what changes is how data moves:
+//
+//   * global -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging, no
+//     ds_write), 1 KiB per wave instruction, swizzle applied on the global side;
+//   * a 2-deep LDS ring: the panel of K-step k+2 streams in while steps k and
+//     k+1 are multiplied; one barrier per K-step, placed so that the MFMA pipe
+//     keeps a k16 slice of work queued across it, and the DMA instructions of
+//     the next panel are interleaved one by one with that slice's MFMAs;
+//   * MFMA operand fragments double-buffered in registers: the LDS reads of
+//     slice s+1 are in flight while slice s is multiplied;
+//   * edge masking by out-of-range buffer offsets (the hardware returns zeros);
+//   * an LDS-staged epilogue: the epilogue operand tile (X or A) is DMA'd into
+//     the freed ring, each lane combines it with its accumulators in place, and
+//     the tile leaves LDS as coalesced 16-byte row chunks (plus the mirrored tile
+//     for the symmetric stages);
+//   * XCD-aware tile order: workgroup w runs on XCD w % 8, so each XCD gets a
+//     contiguous run of tiles that share operand panels in its L2.
+//
+// Used when every 16-byte chunk of X is either fully inside or fully outside
+// the matrix (n % 8 == 0, 16-byte aligned X and Y); the register-staged kernels
+// cover the rest.
+#include "polar_epilogue.hpp"
+#include "polar_kernels.h"
+#include "polar_tile.hpp"
+
+namespace muon_polar {
+
+namespace {
+
+constexpr int kStages = 2;
+
+template <int BM, int BN>
+struct StreamGeom {
+    static constexpr int kABytes = BM * kBK * 2;        // row-operand panel per K-step
+    static constexpr int kBBytes = BN * kBK * 2;        // col-operand panel per K-step
+    static constexpr int kStageBytes = kABytes + kBBytes;
+    static constexpr int kLoadsA = kABytes / 1024 / 4;  // DMA instructions per wave
+    static constexpr int kLoadsB = kBBytes / 1024 / 4;
+    static constexpr int kLoads = kLoadsA + kLoadsB;
+    static constexpr int kTileBytes = BM * BN * 2;      // bf16 output tile (epilogue)
+    static constexpr int kEpiLoads = kTileBytes / 1024 / 4;
+    static_assert(kLoadsA >= 1 && kLoadsB >= 1, "tile too small for 4 waves");
+    static_assert(kTileBytes <= kStages * kStageBytes, "epilogue tile must fit the ring");
+};
+
+// Epilogue tile in LDS: [BM][BN] bf16, 16-byte chunk c of row r stored at chunk
+// position c ^ ((r ^ (r >> 5)) & (BN/8 - 1)).  32 consecutive rows at one chunk
+// (MFMA-layout accesses) and 32 rows spaced 8 apart (mirror reads) both land on
+// distinct chunk positions.
+template <int BN>
+__device__ __forceinline__ int epi_offset(int row, int col) {
+    constexpr int kMask = BN / 8 - 1;
+    return row * BN + ((((col >> 3) ^ ((row ^ (row >> 5)) & kMask))) << 3) + (col & 7);
+}
+
+template <int BM, int BN, Stage S>
+__global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
+    using Geo = StreamGeom<BM, BN>;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int SM = WM / 32, SN = WN / 32;
+    constexpr int kMfmaPerSlice = SM * SN;
+    static_assert(S == Stage::Apply || BM == BN, "triangular stages need square tiles");
+
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * Geo::kStageBytes / 2];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave & 1, wc = wave >> 1;
+
+    // XCD-aware order: the grid is 8 * per_xcd workgroups; XCD x = w % 8 takes
+    // linear tiles [x * per_xcd, (x + 1) * per_xcd).
+    const int w = blockIdx.x;
+    const int tlin = (w & 7) * g.per_xcd + (w >> 3);
+    if (tlin >= g.total_tiles) return;
+    const int bt = tlin / g.tiles_per_batch;
+    const int t = tlin - bt * g.tiles_per_batch;
+    int tm, tn;
+    if constexpr (S == Stage::Apply) {
+        tm = t % g.tiles_m;
+        tn = t / g.tiles_m;
+    } else {
+        upper_tile_of(t, g.tiles_m, tm, tn);
+    }
+    const int row0 = tm * BM, col0 = tn * BN;
+
+    const i32x4 rs_row = make_buffer_rsrc(g.rowop + bt * g.sb_row, g.bytes_row);
+    const i32x4 rs_col = make_buffer_rsrc(g.colop + bt * g.sb_col, g.bytes_col);
+
+    // ------------------------------------------------------------ DMA geometry
+    // Per-lane byte offsets of this wave's DMA chunks at K-step 0 (kOob if the
+    // chunk's row/column lies outside the matrix).
+    constexpr int kBRowsPerInstr = 512 / BN;  // apply: K-rows of X per 1 KiB
+    constexpr int kBLanesPerRow = BN / 8;
+    auto a_row = [&](int i) { return 8 * (wave * Geo::kLoadsA + i) + (lane >> 3); };
+    auto a_chunk = [&](int i) { return (lane & 7) ^ kc_swz(a_row(i)); };
+    auto b_krow = [&](int i) {  // apply
+        return (wave * Geo::kLoadsB + i) * kBRowsPerInstr + lane / kBLanesPerRow;
+    };
+    auto b_row = [&](int i) { return 8 * (wave * Geo::kLoadsB + i) + (lane >> 3); };  // gram/poly
+    auto b_chunk = [&](int i) { return (lane & 7) ^ kc_swz(b_row(i)); };
+
+    uint32_t off_a[Geo::kLoadsA], off_b[Geo::kLoadsB];
+#pragma unroll
+    for (int i = 0; i < Geo::kLoadsA; ++i) {
+        const int gr = row0 + a_row(i);
+        off_a[i] = gr < g.row_rows ? static_cast<uint32_t>((gr * g.ld_row + 8 * a_chunk(i)) * 2)
+                                   : kOob;
+    }
+#pragma unroll
+    for (int i = 0; i < Geo::kLoadsB; ++i) {
+        if constexpr (S == Stage::Apply) {
+            const int krow = b_krow(i);
+            const int c = (lane % kBLanesPerRow) ^ ((krow & 3) << 1);
+            const int col = col0 + 8 * c;
+            off_b[i] = col < g.col_rows ? static_cast<uint32_t>((krow * g.ld_col + col) * 2) : kOob;
+        } else {
+            const int gr = col0 + b_row(i);
+            off_b[i] = gr < g.col_rows ? static_cast<uint32_t>((gr * g.ld_col + 8 * b_chunk(i)) * 2)
+                                       : kOob;
+        }
+    }
+
+    const uint32_t smem_base = lds_addr(smem);
+    auto a_dst = [&](int slot, int i) {
+        return smem_base + slot * Geo::kStageBytes + (wave * Geo::kLoadsA + i) * 1024;
+    };
+    auto b_dst = [&](int slot, int i) {
+        return smem_base + slot * Geo::kStageBytes + Geo::kABytes + (wave * Geo::kLoadsB + i) * 1024;
+    };
+    auto b_step = [&](int k0) -> uint32_t {
+        return static_cast<uint32_t>((S == Stage::Apply ? k0 * g.ld_col : k0) * 2);
+    };
+    // DMA instruction d (0 .. kLoads-1) of K-step `step` into `slot`; `tail`
+    // applies the K-extent masks (only the last K-step can be partial).
+    auto dma_one = [&](int d, int step, int slot, bool tail) {
+        const int k0 = step * kBK;
+        if (d < Geo::kLoadsA) {
+            uint32_t v = off_a[d] + static_cast<uint32_t>(k0 * 2);
+            if (tail && k0 + 8 * a_chunk(d) >= g.row_k) v = kOob;
+            dma_16B(rs_row, a_dst(slot, d), v);
+        } else {
+            const int i = d - Geo::kLoadsA;
+            uint32_t v = off_b[i] + b_step(k0);
+            if (tail) {
+                if constexpr (S == Stage::Apply) {
+                    if (k0 + b_krow(i) >= g.col_k) v = kOob;
+                } else {
+                    if (k0 + 8 * b_chunk(i) >= g.col_k) v = kOob;
+                }
+            }
+            dma_16B(rs_col, b_dst(slot, i), v);
+        }
+    };
+    auto is_tail = [&](int step) {
+        const int k0 = step * kBK;
+        return k0 + kBK > g.row_k || k0 + kBK > g.col_k;
+    };
+    auto issue_all = [&](int step, int slot) {
+        const bool tail = is_tail(step);
+#pragma unroll
+        for (int d = 0; d < Geo::kLoads; ++d) dma_one(d, step, slot, tail);
+    };
+
+    // ------------------------------------------------------------ main loop
+    f32x16 acc[SM][SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // MFMA operand fragments of one k16 slice, double-buffered in registers.
+    auto load_frags = [&](int slot, int kk, bf16x8 (&fr)[SM], bf16x8 (&fc)[SN]) {
+        const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
+        const uint16_t *bs = as + Geo::kABytes / 2;
+#pragma unroll
+        for (int i = 0; i < SM; ++i) fr[i] = frag_kc(as, wr * WM + i * 32 + (lane & 31), kk, lane);
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+            if constexpr (S == Stage::Apply)
+                fc[j] = frag_nc_tr<BN>(bs, wc * WN + j * 32 + ((lane >> 4) & 1) * 16, kk, lane);
+            else
+                fc[j] = frag_kc(bs, wc * WN + j * 32 + (lane & 31), kk, lane);
+        }
+    };
+    auto mfmas = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN]) {
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j) acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
+    };
+    // Last slice of a step: its MFMAs with the DMA of panel `step` interleaved,
+    // about kLoads / kMfmaPerSlice instructions after each MFMA (none when
+    // `active` is false; `tail` applies the K-extent masks of a partial panel).
+    auto mfmas_with_dma = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN], int step, int slot,
+                              bool active, bool tail) {
+#pragma unroll
+        for (int m = 0; m < kMfmaPerSlice; ++m) {
+            const int i = m / SN, j = m % SN;
+            acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int d = m * Geo::kLoads / kMfmaPerSlice; d < (m + 1) * Geo::kLoads / kMfmaPerSlice;
+                 ++d)
+                if (active) dma_one(d, step, slot, tail);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    static_assert(kBK / 16 == 4, "schedule below is written for four k16 slices per step");
+
+    // Schedule per K-step k (slot k%2), slices s0..s3 of 16 K-values:
+    //   frags(s1) | mfma(s0) | frags(s2) | mfma(s1) | frags(s3) | mfma(s2) |
+    //   wait panel k+1, barrier | frags(next s0) | mfma(s3) + DMA panel k+2 -> slot k%2
+    // The barrier sits where every wave has read all of slot k%2 into registers.
+    const int nk = g.k_loop / kBK;
+    bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
+    issue_all(0, 0);
+    if (nk > 1) {
+        issue_all(1, 1);
+        wait_vm_barrier<Geo::kLoads>();
+    } else {
+        wait_vm_barrier<0>();
+    }
+    load_frags(0, 0, fr0, fc0);
+    for (int k = 0; k < nk; ++k) {
+        const int slot = k & 1;
+        load_frags(slot, 1, fr1, fc1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fr0, fc0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_frags(slot, 2, fr0, fc0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fr1, fc1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_frags(slot, 3, fr1, fc1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fr0, fc0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + 1 < nk) {
+            wait_vm_barrier<0>();
+            load_frags(slot ^ 1, 0, fr0, fc0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const bool more = k + 2 < nk;
+        mfmas_with_dma(fr1, fc1, k + 2, slot, more, more && is_tail(k + 2));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ------------------------------------------------------------ epilogue
+    // All waves are done with the ring (and no DMA is outstanding).
+    wait_vm_barrier<0>();
+    uint16_t *tile = smem;
+    uint16_t *out = g.out + bt * g.sb_out;
+    const bool diag = (S != Stage::Apply) && (tm == tn);
+
+    if constexpr (S != Stage::Gram) {
+        // Epilogue operand tile (A for poly, X for apply) -> LDS, rows/cols outside
+        // the matrix read as zero.
+        const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
+        constexpr int kRowsPerInstr = 512 / BN;
+        constexpr int kLanesPerRow = BN / 8;
+#pragma unroll
+        for (int d = 0; d < Geo::kEpiLoads; ++d) {
+            const int blk = wave * Geo::kEpiLoads + d;
+            const int row = blk * kRowsPerInstr + lane / kLanesPerRow;
+            const int p = lane % kLanesPerRow;
+            const int c = p ^ ((row ^ (row >> 5)) & (kLanesPerRow - 1));
+            const int gr = row0 + row, gc = col0 + 8 * c;
+            const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
+                                   ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
+                                   : kOob;
+            dma_16B(rs_epi, smem_base + blk * 1024, v);
+        }
+        wait_vm_barrier<0>();
+    }
+
+    // Each lane turns its accumulators into bf16 results in place.
+#pragma unroll
+    for (int i = 0; i < SM; ++i) {
+        const int r = wr * WM + i * 32 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
+                u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
+                float e[4] = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (S != Stage::Gram) unpack4(*p, e);
+                uint16_t h[4];
+                epilogue_values<S>(acc[i][j], q, e, g, h);
+                *p = pack4(h);
+            }
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // Coalesced store of the tile: 16-byte chunks, consecutive threads along a row.
+    constexpr int kChunksPerRow = BN / 8;
+    for (int idx = tid; idx < BM * kChunksPerRow; idx += 256) {
+        const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
+        const int gr = row0 + row, gc = col0 + 8 * c;
+        if constexpr (S == Stage::Apply) {
+            if (gr >= g.out_rows || gc >= g.out_cols) continue;
+        }
+        u32x4 v;
+        if (!diag) {
+            v = *reinterpret_cast<const u32x4 *>(tile + epi_offset<BN>(row, 8 * c));
+        } else {
+            // Diagonal tile: element (r, c) comes from the upper-triangle source
+            // min/max(r, c), so the stored matrix is bitwise symmetric.
+            uint32_t hh[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int col = 8 * c + e;
+                hh[e] = row <= col ? tile[epi_offset<BN>(row, col)] : tile[epi_offset<BN>(col, row)];
+            }
+            v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
+                      hh[6] | (hh[7] << 16)};
+        }
+        *reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc) = v;
+    }
+
+    // Mirrored store (symmetric stages, off-diagonal tiles): row c of the
+    // mirror tile is column c of this tile; consecutive threads walk along it.
+    if constexpr (S != Stage::Apply) {
+        if (!diag) {
+            constexpr int kMirrorChunks = BM / 8;  // 16-byte chunks per mirror row
+            for (int idx = tid; idx < BN * kMirrorChunks; idx += 256) {
+                const int mc = idx / kMirrorChunks, rb = idx % kMirrorChunks;
+                uint32_t hh[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hh[e] = tile[epi_offset<BN>(8 * rb + e, mc)];
+                const u32x4 v{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
+                              hh[6] | (hh[7] << 16)};
+                *reinterpret_cast<u32x4 *>(out + (col0 + mc) * g.ld_out + row0 + 8 * rb) = v;
+            }
+        }
+    }
+}
+
+template <int BM, int BN, Stage S>
+hipError_t launch_stream_one(const GemmArgs &g, int grid, hipStream_t stream) {
+    GemmArgs copy = g;
+    void *args[] = {&copy};
+    return hipLaunchKernel(reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S>),
+                           dim3(grid), dim3(256), args, 0, stream);
+}
+
+template <Stage S>
+hipError_t launch_stream_by_tile(int bm, int bn, const GemmArgs &g, int grid, hipStream_t stream) {
+    if (bm == 64 && bn == 64) return launch_stream_one<64, 64, S>(g, grid, stream);
+    if (bm == 128 && bn == 128) return launch_stream_one<128, 128, S>(g, grid, stream);
+    if (bm == 256 && bn == 256) return launch_stream_one<256, 256, S>(g, grid, stream);
+    if constexpr (S == Stage::Apply) {
+        if (bm == 128 && bn == 256) return launch_stream_one<128, 256, S>(g, grid, stream);
+        if (bm == 256 && bn == 128) return launch_stream_one<256, 128, S>(g, grid, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_stream(Stage s, int bm, int bn, const GemmArgs &g, hipStream_t stream) {
+    const int grid = 8 * g.per_xcd;
+    switch (s) {
+        case Stage::Gram:
+            return launch_stream_by_tile<Stage::Gram>(bm, bn, g, grid, stream);
+        case Stage::Poly:
+            return launch_stream_by_tile<Stage::Poly>(bm, bn, g, grid, stream);
+        case Stage::Apply:
+            return launch_stream_by_tile<Stage::Apply>(bm, bn, g, grid, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace muon_polar

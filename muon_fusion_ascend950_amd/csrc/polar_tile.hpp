@@ -179,8 +179,79 @@ __device__ __forceinline__ bf16x8 frag_nc_tr(const uint16_t *lds, int n0, int kk
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// Output tile (tm, tn) of linear tile index t within one batch matrix for the
+// triangular stages: row-major walk over the upper tiles tn >= tm of an nt x nt grid.
+__device__ __forceinline__ void upper_tile_of(int t, int nt, int &tm, int &tn) {
+    int row = 0, len = nt;
+    while (t >= len) {
+        t -= len;
+        ++row;
+        --len;
+    }
+    tm = row;
+    tn = row + t;
+}
+
 __device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace muon_polar
+
+// ===========================================================================
+// Direct global -> LDS loads (buffer_load_dwordx4 ... lds) for the streaming
+// kernels.  One wave instruction moves 64 lanes x 16 B = 1 KiB into LDS at
+// M0 + 16*lane, so the LDS image of a tile is chosen by which global chunk each
+// lane fetches (the swizzles above are applied on the global side).  Lanes whose
+// chunk lies outside the matrix use an offset beyond the buffer's num_records:
+// the hardware returns zeros for them, which is how edge tiles are masked.
+// ===========================================================================
+namespace muon_polar {
+
+using i32x4 = int32_t __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kOob = 0x80000000u;  // >= num_records of every buffer (< 2^31 bytes)
+
+// Raw buffer resource (gfx9 family): base, stride 0, num_records in bytes.
+// Arguments must be workgroup-uniform; readfirstlane places the descriptor in
+// SGPRs even when the compiler computed a uniform value in vector registers.
+__device__ __forceinline__ i32x4 make_buffer_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    i32x4 r;
+    r[0] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(b & 0xffffffffu));
+    r[1] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>((b >> 32) & 0xffffu));
+    r[2] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(bytes));
+    r[3] = 0x00020000;
+    return r;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+// 16 B per lane from rsrc+voffset into LDS at lds_base(wave-uniform) + 16*lane.
+// Issued as inline assembly so the compiler neither reorders LDS traffic around
+// it nor inserts its own waits; the kernels wait with vmcnt explicitly.
+__device__ __forceinline__ void dma_16B(i32x4 rsrc, uint32_t lds_base, uint32_t voffset) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voffset), "s"(rsrc)
+                 : "memory", "m0");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding,
+// finish this wave's LDS reads, then workgroup barrier.  The memory clobber keeps
+// the compiler from moving LDS accesses across it.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
 }  // namespace muon_polar

@@ -306,6 +306,8 @@ def test_noncontiguous_input():
     {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_POLY_TILE": "128", "MUON_POLAR_APPLY_TILE_M": "256",
      "MUON_POLAR_APPLY_TILE_N": "128"},
     {"MUON_POLAR_APPLY_TILE_M": "128", "MUON_POLAR_APPLY_TILE_N": "256"},
+    {"MUON_POLAR_STREAM": "0"},
+    {"MUON_POLAR_STREAM": "0", "MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_APPLY_TILE_M": "256"},
 ])
 def test_tile_configuration_does_not_change_results(monkeypatch, env):
     x = O.make_input((2, 300, 1000), seed=11).to(DEV)
@@ -315,6 +317,18 @@ def test_tile_configuration_does_not_change_results(monkeypatch, env):
     other = polar_step(x, *C0)
     torch.cuda.synchronize()
     assert torch.equal(base, other)
+
+
+@pytest.mark.parametrize("shape", [(8, 512, 2048), (1, 1000, 3000), (3, 200, 264), (2, 64, 4096)])
+def test_streaming_and_staged_kernels_agree(monkeypatch, shape):
+    """The DMA-fed kernels and the register-staged kernels accumulate in the same
+    order, so they must agree bit for bit."""
+    x = O.make_input(shape, seed=14).to(DEV)
+    fast = polar_step(x, *C0)
+    monkeypatch.setenv("MUON_POLAR_STREAM", "0")
+    staged = polar_step(x, *C0)
+    torch.cuda.synchronize()
+    assert torch.equal(fast, staged)
 
 
 def test_debug_sync_mode(monkeypatch):
