@@ -273,6 +273,7 @@ int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t b
     g.s_acc = 1.0f;
     g.bytes_row = static_cast<uint32_t>(p.mp * p.mp * 2);
     g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
+    g.group_n = static_cast<int32_t>(std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", 8)));
     const bool vec = (n % 8 == 0) && aligned16(x) && aligned16(y);
     return finish_stage(launch_stage(Stage::Apply, p.apply_bm, p.apply_bn, p.stream && vec, vec,
                                      g, batch, p.apply_grid, stream),

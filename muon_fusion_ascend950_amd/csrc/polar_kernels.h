@@ -30,6 +30,7 @@ struct GemmArgs {
     int32_t total_tiles, per_xcd;   // batch * tiles_per_batch; ceil(total_tiles / 8)
     uint32_t bytes_row, bytes_col;  // byte extent of one batch matrix of rowop / colop
     uint32_t bytes_epi;             // byte extent of one batch matrix of epi
+    int32_t group_n;                // apply: column tiles per raster group
 };
 
 bool tile_supported(Stage s, int bm, int bn);

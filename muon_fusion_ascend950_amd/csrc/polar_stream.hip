@@ -80,8 +80,14 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
     const int t = tlin - bt * g.tiles_per_batch;
     int tm, tn;
     if constexpr (S == Stage::Apply) {
-        tm = t % g.tiles_m;
-        tn = t / g.tiles_m;
+        // Grouped order: runs of group_n column tiles, walked row by row, so the
+        // 32 tiles an XCD holds at once share few P row-panels and X column-panels.
+        const int gn = g.group_n;
+        const int span = gn * g.tiles_m;
+        const int grp = t / span, r = t - grp * span;
+        const int width = min(gn, g.tiles_n - grp * gn);
+        tm = r / width;
+        tn = grp * gn + r % width;
     } else {
         upper_tile_of(t, g.tiles_m, tm, tn);
     }

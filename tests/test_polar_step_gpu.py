@@ -252,7 +252,10 @@ def test_apply_special_cases():
     zero = torch.zeros(1, mp, mp, dtype=torch.bfloat16, device=DEV)
     capi.apply(zero, x, y, a)
     torch.cuda.synchronize()
-    assert torch.equal(y, (x.float() * np.float32(a)).to(torch.bfloat16))
+    # a enters either as an fp32 fma or as a 16-bit-accurate diagonal term: within
+    # one bf16 rounding of a·X
+    want = (x.float() * np.float32(a)).to(torch.bfloat16)
+    assert O.bf16_ulp_distance(bits(y), bits(want)).max() <= 1
     eye = torch.zeros_like(zero)
     eye[0, :100, :100] = torch.eye(100, dtype=torch.bfloat16, device=DEV)
     capi.apply(eye, x, y, 1.0)
@@ -261,10 +264,19 @@ def test_apply_special_cases():
 
 
 # ----------------------------------------------------------------------------- exact properties
-@pytest.mark.parametrize("shape", [(2, 150, 2050), (1, 129, 130), (3, 300, 701)])
-def test_masking_equals_zero_padding(shape):
+def assert_close_kernels(a: torch.Tensor, b: torch.Tensor):
+    """Two kernel paths with different (equally valid) rounding points: normwise
+    agreement to bf16 precision and almost all elements within one bf16 ulp."""
+    an, bn = a.float().cpu().numpy().astype(np.float64), b.float().cpu().numpy().astype(np.float64)
+    assert O.rel_frobenius(an, bn) <= 2e-3
+    assert (O.bf16_ulp_distance(bits(a), bits(b)) > 1).mean() <= 2e-3
+
+
+@pytest.mark.parametrize("shape", [(2, 150, 2050), (1, 129, 130), (3, 300, 701), (2, 100, 512)])
+def test_masking_equals_zero_padding(monkeypatch, shape):
     """Reference binding pads to 128/16 and crops (binding.cpp:630-672); masking must
-    give the same numbers."""
+    give the same numbers: bit for bit within one kernel family, to bf16 precision
+    when the padded shape switches to the DMA-fed kernels."""
     x = O.make_input(shape, seed=7).to(DEV)
     batch, m, n = shape
     rows = -(-m // 128) * 128
@@ -274,7 +286,15 @@ def test_masking_equals_zero_padding(shape):
     y = polar_step(x, *C0)
     yp = polar_step(padded, *C0)[:, :m, :n]
     torch.cuda.synchronize()
-    assert torch.equal(y, yp)
+    if n % 8 == 0:  # same kernel family on both sides
+        assert torch.equal(y, yp)
+    else:
+        assert_close_kernels(y, yp)
+    monkeypatch.setenv("MUON_POLAR_STREAM", "0")
+    ys = polar_step(x, *C0)
+    yps = polar_step(padded, *C0)[:, :m, :n]
+    torch.cuda.synchronize()
+    assert torch.equal(ys, yps)
 
 
 @pytest.mark.parametrize("shape", [(130, 129), (2, 700, 300), (2050, 150)])
@@ -300,16 +320,18 @@ def test_noncontiguous_input():
     assert torch.equal(polar_step(x, *C0), polar_step(x.contiguous(), *C0))
 
 
+@pytest.mark.parametrize("stream", ["1", "0"])
 @pytest.mark.parametrize("env", [
     {"MUON_POLAR_GRAM_TILE": "64", "MUON_POLAR_POLY_TILE": "64", "MUON_POLAR_APPLY_TILE_M": "64"},
     {"MUON_POLAR_GRAM_TILE": "128", "MUON_POLAR_APPLY_TILE_M": "128"},
     {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_POLY_TILE": "128", "MUON_POLAR_APPLY_TILE_M": "256",
      "MUON_POLAR_APPLY_TILE_N": "128"},
     {"MUON_POLAR_APPLY_TILE_M": "128", "MUON_POLAR_APPLY_TILE_N": "256"},
-    {"MUON_POLAR_STREAM": "0"},
-    {"MUON_POLAR_STREAM": "0", "MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_APPLY_TILE_M": "256"},
 ])
-def test_tile_configuration_does_not_change_results(monkeypatch, env):
+def test_tile_configuration_does_not_change_results(monkeypatch, stream, env):
+    """Every tile shape accumulates each output in the same K order, so results are
+    bit-identical across tile configurations of one kernel family."""
+    monkeypatch.setenv("MUON_POLAR_STREAM", stream)
     x = O.make_input((2, 300, 1000), seed=11).to(DEV)
     base = polar_step(x, *C0)
     for k, v in env.items():
@@ -321,14 +343,17 @@ def test_tile_configuration_does_not_change_results(monkeypatch, env):
 
 @pytest.mark.parametrize("shape", [(8, 512, 2048), (1, 1000, 3000), (3, 200, 264), (2, 64, 4096)])
 def test_streaming_and_staged_kernels_agree(monkeypatch, shape):
-    """The DMA-fed kernels and the register-staged kernels accumulate in the same
-    order, so they must agree bit for bit."""
-    x = O.make_input(shape, seed=14).to(DEV)
+    """DMA-fed kernels (diagonal-MFMA epilogue terms) and register-staged kernels
+    (fma epilogues) agree to bf16 precision, and each matches the oracle."""
+    x_cpu = O.make_input(shape, seed=14)
+    x = x_cpu.to(DEV)
     fast = polar_step(x, *C0)
     monkeypatch.setenv("MUON_POLAR_STREAM", "0")
     staged = polar_step(x, *C0)
     torch.cuda.synchronize()
-    assert torch.equal(fast, staged)
+    assert_close_kernels(fast, staged)
+    assert_matches_oracle(fast, x_cpu, [C0], rel_exact=1e-2)
+    assert_matches_oracle(staged, x_cpu, [C0], rel_exact=1e-2)
 
 
 def test_debug_sync_mode(monkeypatch):
