@@ -84,23 +84,28 @@ def kernel_us(fn, launches: int, warmup: int = 3) -> float:
 
 
 def stage_times(batch: int, m: int, n: int, launches: int):
-    """µs per launch of each stage, each launched alone on torch's current stream."""
+    """µs per launch of each stage, each launched alone on torch's current stream,
+    with polar_step's workspace (A and P in it, and the same stream-K split as in
+    the step; a stage call with a workspace also clears its arrival counters, a
+    one-block fill kernel included in its time)."""
     import torch
     from muon_fusion_ascend950_amd import capi
 
     x = make_input((batch, m, n), seed=0).cuda()
-    info = capi.query(batch, m, n)
+    ws, info = capi.alloc_workspace(batch, m, n)
     mp = info.padded_rows
-    gram = torch.empty(batch, mp, mp, dtype=torch.bfloat16, device="cuda")
-    poly = torch.empty_like(gram)
+    p_off = -(-info.gram_bytes // 256) * 256
+    gram = ws[:info.gram_bytes].view(torch.bfloat16).view(batch, mp, mp)
+    poly = ws[p_off:p_off + info.gram_bytes].view(torch.bfloat16).view(batch, mp, mp)
     y = torch.empty_like(x)
     a, b, c = COEFFS
-    capi.gram(x, gram)
-    capi.poly(gram, poly, batch, m, n, b, c)
+    capi.gram(x, gram, workspace=ws)
+    capi.poly(gram, poly, batch, m, n, b, c, workspace=ws)
     return {
-        "gram": kernel_us(lambda: capi.gram(x, gram), launches),
-        "poly": kernel_us(lambda: capi.poly(gram, poly, batch, m, n, b, c), launches),
-        "apply": kernel_us(lambda: capi.apply(poly, x, y, a), launches),
+        "gram": kernel_us(lambda: capi.gram(x, gram, workspace=ws), launches),
+        "poly": kernel_us(lambda: capi.poly(gram, poly, batch, m, n, b, c, workspace=ws),
+                          launches),
+        "apply": kernel_us(lambda: capi.apply(poly, x, y, a, workspace=ws), launches),
     }
 
 

@@ -14,6 +14,15 @@
  * columns of A and P are written as exact zeros by the kernels, so no caller
  * memset is needed.
  *
+ * Stream-K: when the last round of a stage's output tiles would leave most CUs
+ * idle, the K loops of those tiles are cut into equal shares, one per
+ * workgroup, and the last contributor of a tile sums the fp32 partials in a
+ * fixed order (results are the same on every run of one device type, and equal
+ * the unsplit ones to fp32 rounding).  The arrival counters and partial tiles
+ * live in the workspace after A and P; every entry point that gets a workspace
+ * clears the counters it uses itself.  Calls that share one workspace must not
+ * overlap (use one workspace per concurrent stream).
+ *
  * All functions are asynchronous on the given HIP stream (launch only, no
  * synchronisation) unless MUON_POLAR_DEBUG_SYNC is set in the environment, in
  * which case every stage synchronises the stream and reports kernel faults.
@@ -52,7 +61,7 @@ enum muon_polar_status {
 typedef struct muon_polar_shape_info {
     int64_t padded_rows;    /* extent and leading dimension of A and P (>= m) */
     size_t gram_bytes;      /* bytes of one [batch, padded_rows, padded_rows] bf16 buffer */
-    size_t workspace_bytes; /* bytes for A and P together, each 256-byte aligned */
+    size_t workspace_bytes; /* bytes for A and P (each 256-byte aligned) and the stream-K area */
 } muon_polar_shape_info;
 
 int muon_polar_query(int64_t batch, int64_t m, int64_t n, muon_polar_shape_info *info);
@@ -65,25 +74,33 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
                     int64_t batch, int64_t m, int64_t n,
                     double a, double b, double c, hipStream_t stream);
 
+/* The three stages one at a time.  `workspace` is NULL (workspace_bytes
+ * ignored: the stage runs one output tile per workgroup) or a buffer of
+ * info.workspace_bytes, the same one muon_polar_step takes (gram / poly may be
+ * its A / P areas), which lets the stage use the stream-K split exactly as
+ * inside muon_polar_step.  The reference's stage launchers likewise take a
+ * device-side buffer (their tiling struct). */
+
 /* Stage 1: gram[bt] = X[bt]·X[bt]ᵀ into a [batch, padded_rows, padded_rows]
  * bf16 buffer (padding written as zeros).
  * Replaces launch_muon_gram_lowlevel_fused (csrc/muon_polar_step_binding.cpp:65-66,
  * csrc/muon_polar_unified_ascend950.asc:512-517). */
-int muon_polar_gram(const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
-                    hipStream_t stream);
+int muon_polar_gram(const void *x, void *gram, void *workspace, size_t workspace_bytes,
+                    int64_t batch, int64_t m, int64_t n, hipStream_t stream);
 
 /* Stage 2: poly = b·gram + c·gram·gram over [batch, padded_rows, padded_rows];
  * gram must be symmetric (as written by stage 1).
  * Replaces launch_muon_cube2_p_fused (csrc/muon_polar_step_binding.cpp:69-70,
  * csrc/muon_polar_unified_ascend950.asc:1030-1035). */
-int muon_polar_poly(const void *gram, void *poly, int64_t batch, int64_t m, int64_t n,
-                    double b, double c, hipStream_t stream);
+int muon_polar_poly(const void *gram, void *poly, void *workspace, size_t workspace_bytes,
+                    int64_t batch, int64_t m, int64_t n, double b, double c, hipStream_t stream);
 
 /* Stage 3: Y = a·X + poly·X.
  * Replaces launch_muon_cube3_fused_lowlevel (csrc/muon_polar_step_binding.cpp:67-68,
  * csrc/muon_polar_unified_ascend950.asc:1535-1540). */
-int muon_polar_apply(const void *poly, const void *x, void *y, int64_t batch, int64_t m,
-                     int64_t n, double a, hipStream_t stream);
+int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
+                     size_t workspace_bytes, int64_t batch, int64_t m, int64_t n, double a,
+                     hipStream_t stream);
 
 /* Detail of the last failure on the calling thread ("" if none).
  * Replaces CheckAcl / aclGetRecentErrMsg (csrc/muon_polar_step_binding.cpp:72-75). */

@@ -68,9 +68,9 @@ def load() -> ctypes.CDLL:
     i64, vp, sz, dbl = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_double
     lib.muon_polar_query.argtypes = [i64, i64, i64, ctypes.POINTER(ShapeInfo)]
     lib.muon_polar_step.argtypes = [vp, vp, vp, sz, i64, i64, i64, dbl, dbl, dbl, vp]
-    lib.muon_polar_gram.argtypes = [vp, vp, i64, i64, i64, vp]
-    lib.muon_polar_poly.argtypes = [vp, vp, i64, i64, i64, dbl, dbl, vp]
-    lib.muon_polar_apply.argtypes = [vp, vp, vp, i64, i64, i64, dbl, vp]
+    lib.muon_polar_gram.argtypes = [vp, vp, vp, sz, i64, i64, i64, vp]
+    lib.muon_polar_poly.argtypes = [vp, vp, vp, sz, i64, i64, i64, dbl, dbl, vp]
+    lib.muon_polar_apply.argtypes = [vp, vp, vp, vp, sz, i64, i64, i64, dbl, vp]
     for name in ("muon_polar_query", "muon_polar_step", "muon_polar_gram", "muon_polar_poly",
                  "muon_polar_apply"):
         getattr(lib, name).restype = ctypes.c_int
@@ -122,24 +122,32 @@ def alloc_workspace(batch: int, m: int, n: int, device="cuda"):
 def step(x, y, workspace, a: float, b: float, c: float, stream=None) -> None:
     batch, m, n = _bmn(x)
     check("muon_polar_step", load().muon_polar_step(
-        x.data_ptr(), y.data_ptr(), workspace.data_ptr(), workspace.numel(),
+        x.data_ptr(), y.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
         batch, m, n, float(a), float(b), float(c), _stream(stream)))
 
 
-def gram(x, gram_buf, stream=None) -> None:
+def _ws(workspace):
+    """(pointer, bytes) of an optional workspace tensor (None: no stream-K split)."""
+    if workspace is None:
+        return None, 0
+    return workspace.data_ptr(), workspace.numel() * workspace.element_size()
+
+
+def gram(x, gram_buf, stream=None, workspace=None) -> None:
     batch, m, n = _bmn(x)
     check("muon_polar_gram", load().muon_polar_gram(
-        x.data_ptr(), gram_buf.data_ptr(), batch, m, n, _stream(stream)))
+        x.data_ptr(), gram_buf.data_ptr(), *_ws(workspace), batch, m, n, _stream(stream)))
 
 
-def poly(gram_buf, poly_buf, batch: int, m: int, n: int, b: float, c: float, stream=None) -> None:
+def poly(gram_buf, poly_buf, batch: int, m: int, n: int, b: float, c: float, stream=None,
+         workspace=None) -> None:
     check("muon_polar_poly", load().muon_polar_poly(
-        gram_buf.data_ptr(), poly_buf.data_ptr(), batch, m, n, float(b), float(c),
-        _stream(stream)))
+        gram_buf.data_ptr(), poly_buf.data_ptr(), *_ws(workspace), batch, m, n, float(b),
+        float(c), _stream(stream)))
 
 
-def apply(poly_buf, x, y, a: float, stream=None) -> None:
+def apply(poly_buf, x, y, a: float, stream=None, workspace=None) -> None:
     batch, m, n = _bmn(x)
     check("muon_polar_apply", load().muon_polar_apply(
-        poly_buf.data_ptr(), x.data_ptr(), y.data_ptr(), batch, m, n, float(a),
-        _stream(stream)))
+        poly_buf.data_ptr(), x.data_ptr(), y.data_ptr(), *_ws(workspace), batch, m, n,
+        float(a), _stream(stream)))

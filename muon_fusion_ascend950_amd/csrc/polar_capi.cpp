@@ -51,10 +51,11 @@ size_t align256(size_t v) { return (v + 255u) & ~size_t(255u); }
 
 struct Knobs {
     uint32_t gram_tile, poly_tile, apply_bm, apply_bn;
-    uint32_t stream;  // 1: DMA-fed kernels where eligible; 0: register-staged kernels only
+    uint32_t stream;    // 1: DMA-fed kernels where eligible; 0: register-staged kernels only
+    uint32_t stream_k;  // 1: stream-K split of a partial last round (polar_step only); 0: off
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
-               apply_bn == o.apply_bn && stream == o.stream;
+               apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k;
     }
 };
 
@@ -82,8 +83,17 @@ struct PlanKeyHash {
         mix(k.knobs.poly_tile);
         mix(static_cast<uint64_t>(k.knobs.apply_bm) << 32 | k.knobs.apply_bn);
         mix(k.knobs.stream);
+        mix(k.knobs.stream_k);
         return static_cast<size_t>(h);
     }
+};
+
+// Stream-K split of one stage (see GemmArgs): tiles [0, dp_tiles) one per
+// workgroup, the rest cut into sk_units equal ranges of (tile, K-step) iterations.
+struct SkSplit {
+    int64_t dp_tiles;
+    int32_t sk_units;
+    int64_t sk_iters;
 };
 
 struct Plan {
@@ -94,6 +104,13 @@ struct Plan {
     int64_t gram_grid, poly_grid, apply_grid;
     size_t gram_bytes, workspace_bytes;
     bool stream;
+    // polar_step's stream-K splits (gram, poly, apply) and their workspace areas
+    // after A and P: arrival counters (counter_stride words per stage), then
+    // the fp32 partial slots shared by the three stages.
+    SkSplit sk[3];
+    bool sk_any;
+    int64_t counter_stride;
+    size_t counters_offset, partials_offset;
 };
 
 std::mutex g_plan_mutex;
@@ -117,6 +134,8 @@ int read_knobs(int64_t m, int64_t n, Knobs &k) {
     k.apply_bn = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_N", k.apply_bm));
     k.stream = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM", 1));
     if (k.stream > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM must be 0 or 1");
+    k.stream_k = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM_K", 1));
+    if (k.stream_k > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM_K must be 0 or 1");
     if (!muon_polar::tile_supported(Stage::Gram, k.gram_tile, k.gram_tile))
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE must be 64, 128 or 256");
     if (!muon_polar::tile_supported(Stage::Poly, k.poly_tile, k.poly_tile))
@@ -140,6 +159,36 @@ int check_shape(int64_t batch, int64_t m, int64_t n) {
     if (batch > (int64_t(1) << 20))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "batch too large");
     return MUON_POLAR_OK;
+}
+
+// Stream-K for the last round of a stage when it is well under full: with
+// `resident` workgroups in flight, T tiles take ceil(T / resident) rounds one
+// tile per workgroup.  The rem = T % resident tiles of the last round are cut
+// into about `pieces` shares of K-steps each (at most 3, and no more units than
+// resident workgroups), which makes the last round rem * pieces / resident of a
+// round plus the fixup: a tile's last contributor reads the other pieces'
+// partials, so pieces stay few.  Off when the last round is over 3/4 full, when
+// tiles would average under 1.5 pieces, or a share would be under min_share
+// K-steps: a cut tile costs a partial store, the last contributor's partial
+// reads and an epilogue, which shorter shares do not pay back.  Measured on
+// MI355X: with 256x256 tiles (256 KiB partials) 16-step shares lose and 20 and
+// more win or break even; 128x128 tiles (64 KiB partials) gain from 10.
+int64_t sk_min_share(int bm, int bn) { return int64_t(bm) * bn >= 256 * 256 ? 20 : 8; }
+
+SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident,
+                  int64_t min_share) {
+    SkSplit c{tiles, 0, 0};
+    if (!enabled || resident < 8) return c;
+    const int64_t rem = tiles % resident;
+    if (rem == 0 || rem * 4 > resident * 3) return c;
+    const int64_t units = std::min<int64_t>(resident, rem * 3) / 8 * 8;
+    if (units * 2 < rem * 3 || units < 8) return c;
+    const int64_t iters = rem * k_steps;
+    if (iters < min_share * units || iters >= (int64_t(1) << 31)) return c;
+    c.dp_tiles = tiles - rem;
+    c.sk_units = static_cast<int32_t>(units);
+    c.sk_iters = iters;
+    return c;
 }
 
 int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
@@ -171,10 +220,41 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.poly_grid = batch * (int64_t(p.poly_nt) * (p.poly_nt + 1) / 2);
     p.apply_grid = batch * int64_t(p.apply_tm) * p.apply_tn;
     p.gram_bytes = static_cast<size_t>(batch) * p.mp * p.mp * 2u;
-    p.workspace_bytes = 2 * align256(p.gram_bytes);
     p.stream = knobs.stream != 0;
     if (p.gram_grid >= (int64_t(1) << 31) || p.apply_grid >= (int64_t(1) << 31))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "grid too large");
+
+    // Stream-K needs the DMA-fed kernels (X rows of whole 16-byte chunks) and a
+    // device to size the split for.
+    int cus = 0;
+    const bool sk_ok = p.stream && knobs.stream_k != 0 && n % 8 == 0 && device >= 0 &&
+                       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) ==
+                           hipSuccess &&
+                       cus > 0;
+    const int tiles_bm[3] = {p.gram_tile, p.poly_tile, p.apply_bm};
+    const int tiles_bn[3] = {p.gram_tile, p.poly_tile, p.apply_bn};
+    const Stage stages[3] = {Stage::Gram, Stage::Poly, Stage::Apply};
+    const int64_t grids[3] = {p.gram_grid, p.poly_grid, p.apply_grid};
+    const int64_t ksteps[3] = {round_up(n, 64) / 64, p.mp / 64, p.mp / 64};
+    p.sk_any = false;
+    p.counter_stride = 0;
+    size_t partial_bytes = 0;
+    for (int s = 0; s < 3; ++s) {
+        const int occ =
+            sk_ok ? muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s], tiles_bn[s]) : 0;
+        p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ,
+                            sk_min_share(tiles_bm[s], tiles_bn[s]));
+        if (p.sk[s].sk_units > 0) {
+            p.sk_any = true;
+            p.counter_stride = std::max<int64_t>(p.counter_stride, p.sk[s].sk_units);
+            partial_bytes = std::max(partial_bytes, size_t(2) * p.sk[s].sk_units * tiles_bm[s] *
+                                                        tiles_bn[s] * sizeof(float));
+        }
+    }
+    p.counters_offset = 2 * align256(p.gram_bytes);
+    p.partials_offset =
+        p.counters_offset + align256(size_t(3) * p.counter_stride * sizeof(uint32_t));
+    p.workspace_bytes = p.partials_offset + align256(partial_bytes);
     g_plans.emplace(key, p);
     out = p;
     return MUON_POLAR_OK;
@@ -197,17 +277,67 @@ int finish_stage(hipError_t launch, hipStream_t stream, const char *stage) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Workspace areas of polar_step's stream-K splits (null when not splitting:
+// the stage entry points have no workspace and run one tile per workgroup).
+struct SkArea {
+    float *partials;
+    uint32_t *counters;  // this stage's counters
+};
+
 // Launch one stage: DMA-fed kernel when allowed, register-staged otherwise.
 hipError_t launch_stage(Stage s, int bm, int bn, bool stream_ok, bool vec, GemmArgs &g,
-                        int64_t batch, int64_t grid, hipStream_t stream) {
+                        int64_t batch, int64_t grid, const SkSplit *sk, const SkArea *area,
+                        hipStream_t stream) {
     g.total_tiles = static_cast<int32_t>(batch * g.tiles_per_batch);
-    g.per_xcd = (g.total_tiles + 7) / 8;
+    g.k_steps = g.k_loop / 64;
+    g.dp_tiles = g.total_tiles;
+    g.sk_units = 0;
+    g.sk_iters = 0;
+    if (stream_ok && sk != nullptr && area != nullptr && sk->sk_units > 0) {
+        g.dp_tiles = static_cast<int32_t>(sk->dp_tiles);
+        g.sk_units = sk->sk_units;
+        g.sk_iters = sk->sk_iters;
+        g.partials = area->partials;
+        g.counters = area->counters;
+    }
+    g.per_xcd = (g.dp_tiles + 7) / 8;
     if (stream_ok) return muon_polar::launch_stream(s, bm, bn, g, stream);
     return muon_polar::launch_gemm(s, bm, bn, vec, g, static_cast<int>(grid), stream);
 }
 
+SkArea sk_area(const Plan &p, void *workspace, int stage) {
+    char *ws = static_cast<char *>(workspace);
+    return SkArea{reinterpret_cast<float *>(ws + p.partials_offset),
+                  reinterpret_cast<uint32_t *>(ws + p.counters_offset) + stage * p.counter_stride};
+}
+
+int check_workspace(const Plan &p, const void *workspace, size_t workspace_bytes) {
+    if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
+        return fail(MUON_POLAR_ERR_WORKSPACE,
+                    "workspace must hold " + std::to_string(p.workspace_bytes) + " bytes, got " +
+                        std::to_string(workspace == nullptr ? 0 : workspace_bytes));
+    if (!aligned16(workspace))
+        return fail(MUON_POLAR_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+    return MUON_POLAR_OK;
+}
+
+// Stream-K area of one stage call: null without a workspace (no split);
+// otherwise the stage's counters are cleared first.
+int stage_area(const Plan &p, void *workspace, size_t workspace_bytes, int stage, SkArea &area,
+               const SkArea *&out, hipStream_t stream) {
+    out = nullptr;
+    if (workspace == nullptr) return MUON_POLAR_OK;
+    const int st = check_workspace(p, workspace, workspace_bytes);
+    if (st != MUON_POLAR_OK) return st;
+    area = sk_area(p, workspace, stage);
+    out = &area;
+    if (p.sk[stage].sk_units == 0) return MUON_POLAR_OK;
+    return finish_stage(muon_polar::launch_zero_words(area.counters, p.counter_stride, stream),
+                        stream, "counter reset");
+}
+
 int run_gram(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
-             hipStream_t stream) {
+             const SkArea *area, hipStream_t stream) {
     GemmArgs g{};
     g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(x);
     g.out = static_cast<uint16_t *>(gram);
@@ -226,12 +356,12 @@ int run_gram(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m,
     g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
     const bool vec = (n % 8 == 0) && aligned16(x);
     return finish_stage(launch_stage(Stage::Gram, p.gram_tile, p.gram_tile, p.stream && vec, vec,
-                                     g, batch, p.gram_grid, stream),
+                                     g, batch, p.gram_grid, &p.sk[0], area, stream),
                         stream, "gram");
 }
 
 int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double b, double c,
-             hipStream_t stream) {
+             const SkArea *area, hipStream_t stream) {
     GemmArgs g{};
     g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(gram);
     g.out = static_cast<uint16_t *>(poly);
@@ -246,12 +376,12 @@ int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double 
     g.s_acc = static_cast<float>(c);
     g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(p.mp * p.mp * 2);
     return finish_stage(launch_stage(Stage::Poly, p.poly_tile, p.poly_tile, p.stream, true, g,
-                                     batch, p.poly_grid, stream),
+                                     batch, p.poly_grid, &p.sk[1], area, stream),
                         stream, "poly");
 }
 
 int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t batch, int64_t m,
-              int64_t n, double a, hipStream_t stream) {
+              int64_t n, double a, const SkArea *area, hipStream_t stream) {
     GemmArgs g{};
     g.rowop = static_cast<const uint16_t *>(poly);
     g.colop = g.epi = static_cast<const uint16_t *>(x);
@@ -276,7 +406,7 @@ int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t b
     g.group_n = static_cast<int32_t>(std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", 8)));
     const bool vec = (n % 8 == 0) && aligned16(x) && aligned16(y);
     return finish_stage(launch_stage(Stage::Apply, p.apply_bm, p.apply_bn, p.stream && vec, vec,
-                                     g, batch, p.apply_grid, stream),
+                                     g, batch, p.apply_grid, &p.sk[2], area, stream),
                         stream, "apply");
 }
 
@@ -295,38 +425,51 @@ int muon_polar_query(int64_t batch, int64_t m, int64_t n, muon_polar_shape_info 
     return MUON_POLAR_OK;
 }
 
-int muon_polar_gram(const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
-                    hipStream_t stream) {
+int muon_polar_gram(const void *x, void *gram, void *workspace, size_t workspace_bytes,
+                    int64_t batch, int64_t m, int64_t n, hipStream_t stream) {
     if (x == nullptr || gram == nullptr)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
     Plan p{};
-    const int st = get_plan(batch, m, n, p);
+    int st = get_plan(batch, m, n, p);
     if (st != MUON_POLAR_OK) return st;
     if (!aligned16(gram)) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram must be 16-byte aligned");
-    return run_gram(p, x, gram, batch, m, n, stream);
+    SkArea area{};
+    const SkArea *ap = nullptr;
+    st = stage_area(p, workspace, workspace_bytes, 0, area, ap, stream);
+    if (st != MUON_POLAR_OK) return st;
+    return run_gram(p, x, gram, batch, m, n, ap, stream);
 }
 
-int muon_polar_poly(const void *gram, void *poly, int64_t batch, int64_t m, int64_t n, double b,
-                    double c, hipStream_t stream) {
+int muon_polar_poly(const void *gram, void *poly, void *workspace, size_t workspace_bytes,
+                    int64_t batch, int64_t m, int64_t n, double b, double c, hipStream_t stream) {
     if (gram == nullptr || poly == nullptr)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
     Plan p{};
-    const int st = get_plan(batch, m, n, p);
+    int st = get_plan(batch, m, n, p);
     if (st != MUON_POLAR_OK) return st;
     if (!aligned16(gram) || !aligned16(poly))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram and poly must be 16-byte aligned");
-    return run_poly(p, gram, poly, batch, b, c, stream);
+    SkArea area{};
+    const SkArea *ap = nullptr;
+    st = stage_area(p, workspace, workspace_bytes, 1, area, ap, stream);
+    if (st != MUON_POLAR_OK) return st;
+    return run_poly(p, gram, poly, batch, b, c, ap, stream);
 }
 
-int muon_polar_apply(const void *poly, const void *x, void *y, int64_t batch, int64_t m, int64_t n,
-                     double a, hipStream_t stream) {
+int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
+                     size_t workspace_bytes, int64_t batch, int64_t m, int64_t n, double a,
+                     hipStream_t stream) {
     if (poly == nullptr || x == nullptr || y == nullptr)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
     Plan p{};
-    const int st = get_plan(batch, m, n, p);
+    int st = get_plan(batch, m, n, p);
     if (st != MUON_POLAR_OK) return st;
     if (!aligned16(poly)) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "poly must be 16-byte aligned");
-    return run_apply(p, poly, x, y, batch, m, n, a, stream);
+    SkArea area{};
+    const SkArea *ap = nullptr;
+    st = stage_area(p, workspace, workspace_bytes, 2, area, ap, stream);
+    if (st != MUON_POLAR_OK) return st;
+    return run_apply(p, poly, x, y, batch, m, n, a, ap, stream);
 }
 
 int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_bytes, int64_t batch,
@@ -336,19 +479,27 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
     Plan p{};
     int st = get_plan(batch, m, n, p);
     if (st != MUON_POLAR_OK) return st;
-    if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
-        return fail(MUON_POLAR_ERR_WORKSPACE,
-                    "workspace must hold " + std::to_string(p.workspace_bytes) + " bytes, got " +
-                        std::to_string(workspace_bytes));
-    if (!aligned16(workspace))
-        return fail(MUON_POLAR_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+    st = check_workspace(p, workspace, workspace_bytes);
+    if (st != MUON_POLAR_OK) return st;
     void *gram = workspace;
     void *poly = static_cast<char *>(workspace) + align256(p.gram_bytes);
-    st = run_gram(p, x, gram, batch, m, n, stream);
+    if (p.sk_any) {
+        // Arrival counters start at zero; a fill kernel (not a memset node) keeps
+        // the step capturable in a graph.
+        st = finish_stage(
+            muon_polar::launch_zero_words(
+                reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + p.counters_offset),
+                3 * p.counter_stride, stream),
+            stream, "counter reset");
+        if (st != MUON_POLAR_OK) return st;
+    }
+    const SkArea area_gram = sk_area(p, workspace, 0), area_poly = sk_area(p, workspace, 1),
+                 area_apply = sk_area(p, workspace, 2);
+    st = run_gram(p, x, gram, batch, m, n, &area_gram, stream);
     if (st != MUON_POLAR_OK) return st;
-    st = run_poly(p, gram, poly, batch, b, c, stream);
+    st = run_poly(p, gram, poly, batch, b, c, &area_poly, stream);
     if (st != MUON_POLAR_OK) return st;
-    return run_apply(p, poly, x, y, batch, m, n, a, stream);
+    return run_apply(p, poly, x, y, batch, m, n, a, &area_apply, stream);
 }
 
 const char *muon_polar_last_error(void) { return g_last_error.c_str(); }

@@ -27,10 +27,22 @@ struct GemmArgs {
     int32_t tiles_m, tiles_n, tiles_per_batch;
     float s_epi, s_acc;  // poly: b, c;  apply: a, 1
     // streaming kernels only
-    int32_t total_tiles, per_xcd;   // batch * tiles_per_batch; ceil(total_tiles / 8)
+    int32_t total_tiles, per_xcd;   // batch * tiles_per_batch; ceil(dp_tiles / 8)
     uint32_t bytes_row, bytes_col;  // byte extent of one batch matrix of rowop / colop
     uint32_t bytes_epi;             // byte extent of one batch matrix of epi
     int32_t group_n;                // apply: column tiles per raster group
+    // Stream-K split of the streaming kernels.  Tiles [0, dp_tiles) run one per
+    // workgroup (the first 8 * per_xcd workgroups); tiles [dp_tiles, total_tiles)
+    // form sk_iters = (total_tiles - dp_tiles) * k_steps (tile, K-step)
+    // iterations cut into sk_units equal contiguous ranges, one per workgroup
+    // after those.  A tile cut between ranges is summed from fp32 partials by the
+    // last contributor to arrive.
+    int32_t k_steps;                // k_loop / 64
+    int32_t dp_tiles;               // == total_tiles when stream-K is off
+    int32_t sk_units;               // 0 or a multiple of 8
+    int64_t sk_iters;
+    float *partials;                // 2 * sk_units slots of BM * BN floats
+    uint32_t *counters;             // one arrival counter per stream-K tile, zero on entry
 };
 
 bool tile_supported(Stage s, int bm, int bn);
@@ -40,7 +52,13 @@ hipError_t launch_gemm(Stage s, int bm, int bn, bool vec, const GemmArgs &g, int
                        hipStream_t stream);
 
 // DMA-fed kernels: X chunks of 16 B must be entirely inside or outside the matrix
-// (n % 8 == 0, 16-byte aligned X).  Grid is 8 * g.per_xcd.
+// (n % 8 == 0, 16-byte aligned X).  Grid is g.sk_units + 8 * g.per_xcd.
 hipError_t launch_stream(Stage s, int bm, int bn, const GemmArgs &g, hipStream_t stream);
+
+// Workgroups of the DMA-fed kernel for (s, bm, bn) resident per CU (0 on error).
+int stream_blocks_per_cu(Stage s, int bm, int bn);
+
+// Sets n 32-bit words at p to zero (stream-ordered, no memset node).
+hipError_t launch_zero_words(uint32_t *p, int64_t n, hipStream_t stream);
 
 }  // namespace muon_polar

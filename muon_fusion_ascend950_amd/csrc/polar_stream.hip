@@ -56,6 +56,22 @@ __device__ __forceinline__ int epi_offset(int row, int col) {
     return row * BN + ((((col >> 3) ^ ((row ^ (row >> 5)) & kMask))) << 3) + (col & 7);
 }
 
+// Stream-K bookkeeping (all values uniform across the workgroup).
+// Range of unit u: iterations [sk_bound(u), sk_bound(u + 1)).
+__device__ __forceinline__ int64_t sk_bound(const GemmArgs &g, int u) {
+    return int64_t(u) * g.sk_iters / g.sk_units;
+}
+// Unit whose range holds iteration i: the largest u with sk_bound(u) <= i.
+__device__ __forceinline__ int sk_unit_of(const GemmArgs &g, int64_t i) {
+    const int64_t u = ((i + 1) * g.sk_units - 1) / g.sk_iters;
+    return u < g.sk_units ? static_cast<int>(u) : g.sk_units - 1;
+}
+// Partial slot of unit u for stream-K tile st: 2u for the first tile of its
+// range, 2u + 1 for the last one (only those two can be cut).
+__device__ __forceinline__ int sk_slot(const GemmArgs &g, int u, int st) {
+    return 2 * u + (st != static_cast<int>(sk_bound(g, u) / g.k_steps));
+}
+
 template <int BM, int BN, Stage S>
 __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
     using Geo = StreamGeom<BM, BN>;
@@ -65,288 +81,424 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
     static_assert(S == Stage::Apply || BM == BN, "triangular stages need square tiles");
 
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * Geo::kStageBytes / 2];
+    __shared__ uint32_t s_arrived;
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int wr = wave & 1, wc = wave >> 1;
+    const int nk = g.k_steps;
+    const uint32_t smem_base = lds_addr(smem);
 
-    // XCD-aware order: the grid is 8 * per_xcd workgroups; XCD x = w % 8 takes
-    // linear tiles [x * per_xcd, (x + 1) * per_xcd).
+    // Work of this workgroup: iterations [it_lo, it_hi) of tiles tile_base + i / nk.
+    // Workgroup w runs on XCD w % 8; each XCD gets a contiguous run of whole
+    // tiles (workgroups [0, 8 * per_xcd), dispatched first, so full rounds start
+    // together and tiles that share operand panels stay in step) and of
+    // stream-K units (the rest, which fill the last round as CUs free up).
     const int w = blockIdx.x;
-    const int tlin = (w & 7) * g.per_xcd + (w >> 3);
-    if (tlin >= g.total_tiles) return;
-    const int bt = tlin / g.tiles_per_batch;
-    const int t = tlin - bt * g.tiles_per_batch;
-    int tm, tn;
-    if constexpr (S == Stage::Apply) {
-        // Grouped order: runs of group_n column tiles, walked row by row, so the
-        // 32 tiles an XCD holds at once share few P row-panels and X column-panels.
-        const int gn = g.group_n;
-        const int span = gn * g.tiles_m;
-        const int grp = t / span, r = t - grp * span;
-        const int width = min(gn, g.tiles_n - grp * gn);
-        tm = r / width;
-        tn = grp * gn + r % width;
+    const int dp_grid = 8 * g.per_xcd;
+    int unit = -1, tile_base;
+    int64_t it_lo, it_hi;
+    if (w >= dp_grid) {
+        const int ws = w - dp_grid;
+        unit = (ws & 7) * (g.sk_units >> 3) + (ws >> 3);
+        tile_base = g.dp_tiles;
+        it_lo = sk_bound(g, unit);
+        it_hi = sk_bound(g, unit + 1);
     } else {
-        upper_tile_of(t, g.tiles_m, tm, tn);
+        tile_base = (w & 7) * g.per_xcd + (w >> 3);
+        if (tile_base >= g.dp_tiles) return;
+        it_lo = 0;
+        it_hi = nk;
     }
-    const int row0 = tm * BM, col0 = tn * BN;
 
-    const i32x4 rs_row = make_buffer_rsrc(g.rowop + bt * g.sb_row, g.bytes_row);
-    const i32x4 rs_col = make_buffer_rsrc(g.colop + bt * g.sb_col, g.bytes_col);
+    // Segments are taken from the end of the range backwards: a unit first
+    // computes the leading K-steps of its last tile (a partial the tile's owner
+    // of the final K-steps will need) and ends with the trailing K-steps of its
+    // first tile, so the contributor that arrives last usually finds the other
+    // partials long written.
+    for (int64_t hi = it_hi; hi > it_lo;) {
+        const int lt = static_cast<int>((hi - 1) / nk);
+        const int64_t tstart = int64_t(lt) * nk;
+        const int64_t lo = tstart > it_lo ? tstart : it_lo;
+        const int kbeg = static_cast<int>(lo - tstart), kend = static_cast<int>(hi - tstart);
+        if (hi != it_hi) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        hi = lo;
+        // The thread index is opaque to the optimizer from here on, so the many
+        // per-lane offsets derived from it are formed inside each segment instead
+        // of being kept (and spilled) across the segment loop.
+        int tid = static_cast<int>(threadIdx.x);
+        asm volatile("" : "+v"(tid));
+        const int lane = tid & 63;
 
-    // ------------------------------------------------------------ DMA geometry
-    // Per-lane byte offsets of this wave's DMA chunks at K-step 0 (kOob if the
-    // chunk's row/column lies outside the matrix).
-    constexpr int kBRowsPerInstr = 512 / BN;  // apply: K-rows of X per 1 KiB
-    constexpr int kBLanesPerRow = BN / 8;
-    auto a_row = [&](int i) { return 8 * (wave * Geo::kLoadsA + i) + (lane >> 3); };
-    auto a_chunk = [&](int i) { return (lane & 7) ^ kc_swz(a_row(i)); };
-    auto b_krow = [&](int i) {  // apply
-        return (wave * Geo::kLoadsB + i) * kBRowsPerInstr + lane / kBLanesPerRow;
-    };
-    auto b_row = [&](int i) { return 8 * (wave * Geo::kLoadsB + i) + (lane >> 3); };  // gram/poly
-    auto b_chunk = [&](int i) { return (lane & 7) ^ kc_swz(b_row(i)); };
-
-    uint32_t off_a[Geo::kLoadsA], off_b[Geo::kLoadsB];
-#pragma unroll
-    for (int i = 0; i < Geo::kLoadsA; ++i) {
-        const int gr = row0 + a_row(i);
-        off_a[i] = gr < g.row_rows ? static_cast<uint32_t>((gr * g.ld_row + 8 * a_chunk(i)) * 2)
-                                   : kOob;
-    }
-#pragma unroll
-    for (int i = 0; i < Geo::kLoadsB; ++i) {
+        const int tlin = tile_base + lt;
+        const int bt = tlin / g.tiles_per_batch;
+        const int t = tlin - bt * g.tiles_per_batch;
+        int tm, tn;
         if constexpr (S == Stage::Apply) {
-            const int krow = b_krow(i);
-            const int c = (lane % kBLanesPerRow) ^ ((krow & 3) << 1);
-            const int col = col0 + 8 * c;
-            off_b[i] = col < g.col_rows ? static_cast<uint32_t>((krow * g.ld_col + col) * 2) : kOob;
+            // Grouped order: runs of group_n column tiles, walked row by row, so the
+            // tiles an XCD holds at once share few P row-panels and X column-panels.
+            const int gn = g.group_n;
+            const int span = gn * g.tiles_m;
+            const int grp = t / span, r = t - grp * span;
+            const int width = min(gn, g.tiles_n - grp * gn);
+            tm = r / width;
+            tn = grp * gn + r % width;
         } else {
-            const int gr = col0 + b_row(i);
-            off_b[i] = gr < g.col_rows ? static_cast<uint32_t>((gr * g.ld_col + 8 * b_chunk(i)) * 2)
+            upper_tile_of(t, g.tiles_m, tm, tn);
+        }
+        const int row0 = tm * BM, col0 = tn * BN;
+
+        const i32x4 rs_row = make_buffer_rsrc(g.rowop + bt * g.sb_row, g.bytes_row);
+        const i32x4 rs_col = make_buffer_rsrc(g.colop + bt * g.sb_col, g.bytes_col);
+
+        // -------------------------------------------------------- DMA geometry
+        // Per-lane byte offsets of this wave's DMA chunks at K-step 0 (kOob if the
+        // chunk's row/column lies outside the matrix).
+        constexpr int kBRowsPerInstr = 512 / BN;  // apply: K-rows of X per 1 KiB
+        constexpr int kBLanesPerRow = BN / 8;
+        auto a_row = [&](int i) { return 8 * (wave * Geo::kLoadsA + i) + (lane >> 3); };
+        auto a_chunk = [&](int i) { return (lane & 7) ^ kc_swz(a_row(i)); };
+        auto b_krow = [&](int i) {  // apply
+            return (wave * Geo::kLoadsB + i) * kBRowsPerInstr + lane / kBLanesPerRow;
+        };
+        auto b_row = [&](int i) { return 8 * (wave * Geo::kLoadsB + i) + (lane >> 3); };  // gram/poly
+        auto b_chunk = [&](int i) { return (lane & 7) ^ kc_swz(b_row(i)); };
+
+        uint32_t off_a[Geo::kLoadsA], off_b[Geo::kLoadsB];
+#pragma unroll
+        for (int i = 0; i < Geo::kLoadsA; ++i) {
+            const int gr = row0 + a_row(i);
+            off_a[i] = gr < g.row_rows ? static_cast<uint32_t>((gr * g.ld_row + 8 * a_chunk(i)) * 2)
                                        : kOob;
         }
-    }
-
-    const uint32_t smem_base = lds_addr(smem);
-    auto a_dst = [&](int slot, int i) {
-        return smem_base + slot * Geo::kStageBytes + (wave * Geo::kLoadsA + i) * 1024;
-    };
-    auto b_dst = [&](int slot, int i) {
-        return smem_base + slot * Geo::kStageBytes + Geo::kABytes + (wave * Geo::kLoadsB + i) * 1024;
-    };
-    auto b_step = [&](int k0) -> uint32_t {
-        return static_cast<uint32_t>((S == Stage::Apply ? k0 * g.ld_col : k0) * 2);
-    };
-    // DMA instruction d (0 .. kLoads-1) of K-step `step` into `slot`; `tail`
-    // applies the K-extent masks (only the last K-step can be partial).
-    auto dma_one = [&](int d, int step, int slot, bool tail) {
-        const int k0 = step * kBK;
-        if (d < Geo::kLoadsA) {
-            uint32_t v = off_a[d] + static_cast<uint32_t>(k0 * 2);
-            if (tail && k0 + 8 * a_chunk(d) >= g.row_k) v = kOob;
-            dma_16B(rs_row, a_dst(slot, d), v);
-        } else {
-            const int i = d - Geo::kLoadsA;
-            uint32_t v = off_b[i] + b_step(k0);
-            if (tail) {
-                if constexpr (S == Stage::Apply) {
-                    if (k0 + b_krow(i) >= g.col_k) v = kOob;
-                } else {
-                    if (k0 + 8 * b_chunk(i) >= g.col_k) v = kOob;
-                }
+#pragma unroll
+        for (int i = 0; i < Geo::kLoadsB; ++i) {
+            if constexpr (S == Stage::Apply) {
+                const int krow = b_krow(i);
+                const int c = (lane % kBLanesPerRow) ^ ((krow & 3) << 1);
+                const int col = col0 + 8 * c;
+                off_b[i] =
+                    col < g.col_rows ? static_cast<uint32_t>((krow * g.ld_col + col) * 2) : kOob;
+            } else {
+                const int gr = col0 + b_row(i);
+                off_b[i] = gr < g.col_rows
+                               ? static_cast<uint32_t>((gr * g.ld_col + 8 * b_chunk(i)) * 2)
+                               : kOob;
             }
-            dma_16B(rs_col, b_dst(slot, i), v);
         }
-    };
-    auto is_tail = [&](int step) {
-        const int k0 = step * kBK;
-        return k0 + kBK > g.row_k || k0 + kBK > g.col_k;
-    };
-    auto issue_all = [&](int step, int slot) {
-        const bool tail = is_tail(step);
-#pragma unroll
-        for (int d = 0; d < Geo::kLoads; ++d) dma_one(d, step, slot, tail);
-    };
 
-    // ------------------------------------------------------------ main loop
-    f32x16 acc[SM][SN];
+        auto a_dst = [&](int slot, int i) {
+            return smem_base + slot * Geo::kStageBytes + (wave * Geo::kLoadsA + i) * 1024;
+        };
+        auto b_dst = [&](int slot, int i) {
+            return smem_base + slot * Geo::kStageBytes + Geo::kABytes +
+                   (wave * Geo::kLoadsB + i) * 1024;
+        };
+        auto b_step = [&](int k0) -> uint32_t {
+            return static_cast<uint32_t>((S == Stage::Apply ? k0 * g.ld_col : k0) * 2);
+        };
+        // DMA instruction d (0 .. kLoads-1) of K-step `step` into `slot`; `tail`
+        // applies the K-extent masks (only the last K-step can be partial).
+        auto dma_one = [&](int d, int step, int slot, bool tail) {
+            const int k0 = step * kBK;
+            if (d < Geo::kLoadsA) {
+                uint32_t v = off_a[d] + static_cast<uint32_t>(k0 * 2);
+                if (tail && k0 + 8 * a_chunk(d) >= g.row_k) v = kOob;
+                dma_16B(rs_row, a_dst(slot, d), v);
+            } else {
+                const int i = d - Geo::kLoadsA;
+                uint32_t v = off_b[i] + b_step(k0);
+                if (tail) {
+                    if constexpr (S == Stage::Apply) {
+                        if (k0 + b_krow(i) >= g.col_k) v = kOob;
+                    } else {
+                        if (k0 + 8 * b_chunk(i) >= g.col_k) v = kOob;
+                    }
+                }
+                dma_16B(rs_col, b_dst(slot, i), v);
+            }
+        };
+        auto is_tail = [&](int step) {
+            const int k0 = step * kBK;
+            return k0 + kBK > g.row_k || k0 + kBK > g.col_k;
+        };
+        auto issue_all = [&](int step, int slot) {
+            const bool tail = is_tail(step);
 #pragma unroll
-    for (int i = 0; i < SM; ++i)
-#pragma unroll
-        for (int j = 0; j < SN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+            for (int d = 0; d < Geo::kLoads; ++d) dma_one(d, step, slot, tail);
+        };
 
-    // MFMA operand fragments of one k16 slice, double-buffered in registers.
-    auto load_frags = [&](int slot, int kk, bf16x8 (&fr)[SM], bf16x8 (&fc)[SN]) {
-        const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
-        const uint16_t *bs = as + Geo::kABytes / 2;
-#pragma unroll
-        for (int i = 0; i < SM; ++i) fr[i] = frag_kc(as, wr * WM + i * 32 + (lane & 31), kk, lane);
-#pragma unroll
-        for (int j = 0; j < SN; ++j) {
-            if constexpr (S == Stage::Apply)
-                fc[j] = frag_nc_tr<BN>(bs, wc * WN + j * 32 + ((lane >> 4) & 1) * 16, kk, lane);
-            else
-                fc[j] = frag_kc(bs, wc * WN + j * 32 + (lane & 31), kk, lane);
-        }
-    };
-    auto mfmas = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN]) {
+        // -------------------------------------------------------- main loop
+        f32x16 acc[SM][SN];
 #pragma unroll
         for (int i = 0; i < SM; ++i)
 #pragma unroll
-            for (int j = 0; j < SN; ++j) acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
-    };
-    // Last slice of a step: its MFMAs with the DMA of panel `step` interleaved,
-    // about kLoads / kMfmaPerSlice instructions after each MFMA (none when
-    // `active` is false; `tail` applies the K-extent masks of a partial panel).
-    auto mfmas_with_dma = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN], int step, int slot,
-                              bool active, bool tail) {
+            for (int j = 0; j < SN; ++j)
 #pragma unroll
-        for (int m = 0; m < kMfmaPerSlice; ++m) {
-            const int i = m / SN, j = m % SN;
-            acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int d = m * Geo::kLoads / kMfmaPerSlice; d < (m + 1) * Geo::kLoads / kMfmaPerSlice;
-                 ++d)
-                if (active) dma_one(d, step, slot, tail);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    static_assert(kBK / 16 == 4, "schedule below is written for four k16 slices per step");
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // Schedule per K-step k (slot k%2), slices s0..s3 of 16 K-values:
-    //   frags(s1) | mfma(s0) | frags(s2) | mfma(s1) | frags(s3) | mfma(s2) |
-    //   wait panel k+1, barrier | frags(next s0) | mfma(s3) + DMA panel k+2 -> slot k%2
-    // The barrier sits where every wave has read all of slot k%2 into registers.
-    const int nk = g.k_loop / kBK;
-    bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
-    issue_all(0, 0);
-    if (nk > 1) {
-        issue_all(1, 1);
-        wait_vm_barrier<Geo::kLoads>();
-    } else {
-        wait_vm_barrier<0>();
-    }
-    load_frags(0, 0, fr0, fc0);
-    for (int k = 0; k < nk; ++k) {
-        const int slot = k & 1;
-        load_frags(slot, 1, fr1, fc1);
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(fr0, fc0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_frags(slot, 2, fr0, fc0);
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(fr1, fc1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_frags(slot, 3, fr1, fc1);
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(fr0, fc0);
-        __builtin_amdgcn_sched_barrier(0);
-        if (k + 1 < nk) {
-            wait_vm_barrier<0>();
-            load_frags(slot ^ 1, 0, fr0, fc0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const bool more = k + 2 < nk;
-        mfmas_with_dma(fr1, fc1, k + 2, slot, more, more && is_tail(k + 2));
-        __builtin_amdgcn_sched_barrier(0);
-    }
-
-    // ------------------------------------------------------------ epilogue
-    // All waves are done with the ring (and no DMA is outstanding).
-    wait_vm_barrier<0>();
-    uint16_t *tile = smem;
-    uint16_t *out = g.out + bt * g.sb_out;
-    const bool diag = (S != Stage::Apply) && (tm == tn);
-
-    if constexpr (S != Stage::Gram) {
-        // Epilogue operand tile (A for poly, X for apply) -> LDS, rows/cols outside
-        // the matrix read as zero.
-        const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
-        constexpr int kRowsPerInstr = 512 / BN;
-        constexpr int kLanesPerRow = BN / 8;
+        // MFMA operand fragments of one k16 slice, double-buffered in registers.
+        auto load_frags = [&](int slot, int kk, bf16x8 (&fr)[SM], bf16x8 (&fc)[SN]) {
+            const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
+            const uint16_t *bs = as + Geo::kABytes / 2;
 #pragma unroll
-        for (int d = 0; d < Geo::kEpiLoads; ++d) {
-            const int blk = wave * Geo::kEpiLoads + d;
-            const int row = blk * kRowsPerInstr + lane / kLanesPerRow;
-            const int p = lane % kLanesPerRow;
-            const int c = p ^ ((row ^ (row >> 5)) & (kLanesPerRow - 1));
-            const int gr = row0 + row, gc = col0 + 8 * c;
-            const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
-                                   ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
-                                   : kOob;
-            dma_16B(rs_epi, smem_base + blk * 1024, v);
-        }
-        wait_vm_barrier<0>();
-    }
-
-    // Each lane turns its accumulators into bf16 results in place.
+            for (int i = 0; i < SM; ++i)
+                fr[i] = frag_kc(as, wr * WM + i * 32 + (lane & 31), kk, lane);
 #pragma unroll
-    for (int i = 0; i < SM; ++i) {
-        const int r = wr * WM + i * 32 + (lane & 31);
-#pragma unroll
-        for (int j = 0; j < SN; ++j) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
-                u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
-                float e[4] = {0.f, 0.f, 0.f, 0.f};
-                if constexpr (S != Stage::Gram) unpack4(*p, e);
-                uint16_t h[4];
-                epilogue_values<S>(acc[i][j], q, e, g, h);
-                *p = pack4(h);
+            for (int j = 0; j < SN; ++j) {
+                if constexpr (S == Stage::Apply)
+                    fc[j] = frag_nc_tr<BN>(bs, wc * WN + j * 32 + ((lane >> 4) & 1) * 16, kk, lane);
+                else
+                    fc[j] = frag_kc(bs, wc * WN + j * 32 + (lane & 31), kk, lane);
             }
-        }
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        };
+        auto mfmas = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN]) {
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+#pragma unroll
+                for (int j = 0; j < SN; ++j) acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
+        };
+        // Last slice of a step: its MFMAs with the DMA of panel `step` interleaved,
+        // about kLoads / kMfmaPerSlice instructions after each MFMA (none when
+        // `active` is false; `tail` applies the K-extent masks of a partial panel).
+        auto mfmas_with_dma = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN], int step,
+                                  int slot, bool active, bool tail) {
+#pragma unroll
+            for (int m = 0; m < kMfmaPerSlice; ++m) {
+                const int i = m / SN, j = m % SN;
+                acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int d = m * Geo::kLoads / kMfmaPerSlice;
+                     d < (m + 1) * Geo::kLoads / kMfmaPerSlice; ++d)
+                    if (active) dma_one(d, step, slot, tail);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        static_assert(kBK / 16 == 4, "schedule below is written for four k16 slices per step");
 
-    // Coalesced store of the tile: 16-byte chunks, consecutive threads along a row.
-    constexpr int kChunksPerRow = BN / 8;
-    for (int idx = tid; idx < BM * kChunksPerRow; idx += 256) {
-        const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
-        const int gr = row0 + row, gc = col0 + 8 * c;
-        if constexpr (S == Stage::Apply) {
-            if (gr >= g.out_rows || gc >= g.out_cols) continue;
-        }
-        u32x4 v;
-        if (!diag) {
-            v = *reinterpret_cast<const u32x4 *>(tile + epi_offset<BN>(row, 8 * c));
+        // Schedule per K-step k (slot k%2), slices s0..s3 of 16 K-values:
+        //   frags(s1) | mfma(s0) | frags(s2) | mfma(s1) | frags(s3) | mfma(s2) |
+        //   wait panel k+1, barrier | frags(next s0) | mfma(s3) + DMA panel k+2 -> slot k%2
+        // The barrier sits where every wave has read all of slot k%2 into registers.
+        const int nkl = kend - kbeg;
+        bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
+        issue_all(kbeg, 0);
+        if (nkl > 1) {
+            issue_all(kbeg + 1, 1);
+            wait_vm_barrier<Geo::kLoads>();
         } else {
-            // Diagonal tile: element (r, c) comes from the upper-triangle source
-            // min/max(r, c), so the stored matrix is bitwise symmetric.
-            uint32_t hh[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int col = 8 * c + e;
-                hh[e] = row <= col ? tile[epi_offset<BN>(row, col)] : tile[epi_offset<BN>(col, row)];
-            }
-            v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
-                      hh[6] | (hh[7] << 16)};
+            wait_vm_barrier<0>();
         }
-        *reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc) = v;
-    }
+        load_frags(0, 0, fr0, fc0);
+        for (int k = 0; k < nkl; ++k) {
+            const int slot = k & 1;
+            load_frags(slot, 1, fr1, fc1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(fr0, fc0);
+            __builtin_amdgcn_sched_barrier(0);
+            load_frags(slot, 2, fr0, fc0);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(fr1, fc1);
+            __builtin_amdgcn_sched_barrier(0);
+            load_frags(slot, 3, fr1, fc1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(fr0, fc0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + 1 < nkl) {
+                wait_vm_barrier<0>();
+                load_frags(slot ^ 1, 0, fr0, fc0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const bool more = k + 2 < nkl;
+            mfmas_with_dma(fr1, fc1, kbeg + k + 2, slot, more, more && is_tail(kbeg + k + 2));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // All waves are done with the ring (and no DMA is outstanding).
+        wait_vm_barrier<0>();
 
-    // Mirrored store (symmetric stages, off-diagonal tiles): row c of the
-    // mirror tile is column c of this tile; consecutive threads walk along it.
-    if constexpr (S != Stage::Apply) {
-        if (!diag) {
-            constexpr int kMirrorChunks = BM / 8;  // 16-byte chunks per mirror row
-            for (int idx = tid; idx < BN * kMirrorChunks; idx += 256) {
-                const int mc = idx / kMirrorChunks, rb = idx % kMirrorChunks;
+        // -------------------------------------------------------- stream-K fixup
+        if (kbeg != 0 || kend != nk) {
+            // This tile is cut between units u0 .. u1.  Each contributor but the
+            // last stores its fp32 partial and counts itself in; the last one to
+            // arrive forms p(u1) + p(u1 - 1) + ... + p(u0) in that fixed order (so
+            // results do not depend on arrival order) and runs the epilogue.
+            const int u0 = sk_unit_of(g, tstart), u1 = sk_unit_of(g, tstart + nk - 1);
+            const uint32_t others = static_cast<uint32_t>(u1 - u0);
+            uint32_t *cnt = g.counters + lt;
+            // Partials and counters are accessed device-coherently (sc1 stores and
+            // loads, agent-scope atomics), so no whole-cache write-back or
+            // invalidate is needed: a contributor's stores are complete before its
+            // count is added, and the last contributor reads them after seeing
+            // every count.  The L2 contents the other workgroups are streaming
+            // from stay intact.
+            constexpr int kSc1 = 16;  // cache-policy bits of a device-scope access
+            const int64_t slot_bytes = int64_t(BM) * BN * 4;
+            const __amdgpu_buffer_rsrc_t rs_part =
+                __builtin_amdgcn_make_buffer_rsrc(g.partials, 0, 0x7fffffff, 0x00020000);
+            auto lane_base = [&](int u) {
+                return static_cast<uint32_t>(int64_t(sk_slot(g, u, lt)) * slot_bytes) + tid * 16;
+            };
+            // Slot layout: 16-byte chunk c = (i * SN + j) * 4 + q of every thread,
+            // thread-minor, so each access instruction covers 4 KiB contiguously.
+            auto store_own = [&]() {
+                const uint32_t base = lane_base(unit);
+#pragma unroll
+                for (int i = 0; i < SM; ++i)
+#pragma unroll
+                    for (int j = 0; j < SN; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            __builtin_amdgcn_raw_buffer_store_b128(
+                                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                      acc[i][j][4 * q + 3]},
+                                rs_part, base + ((i * SN + j) * 4 + q) * 4096, 0, kSc1);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            };
+            if (tid == 0)
+                s_arrived = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            bool last = __builtin_amdgcn_readfirstlane(s_arrived) == others;
+            bool stored = false;
+            if (!last) {
+                store_own();
+                stored = true;
+                __syncthreads();
+                if (tid == 0)
+                    s_arrived =
+                        __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __syncthreads();
+                last = __builtin_amdgcn_readfirstlane(s_arrived) == others;
+            }
+            if (!last) continue;
+            // Own partial first or second in the order: add the others to it in
+            // place (x + y == y + x).  Further back: start from p(u1) in memory.
+            const bool from_memory = u1 - unit >= 2;
+            if (from_memory && !stored) store_own();  // read back by the same lanes
+            // Partials are read a row-block (16 chunks per lane) at a time, the
+            // next block's loads in flight while the current one is added.
+            auto add_partial = [&](int u, bool assign) {
+                const uint32_t base = lane_base(u);
+                f32x4 x[2][SN * 4];
+                auto load_block = [&](int i, f32x4 (&dst)[SN * 4]) {
+#pragma unroll
+                    for (int c = 0; c < SN * 4; ++c)
+                        dst[c] = __builtin_amdgcn_raw_buffer_load_b128(
+                            rs_part, base + (i * SN * 4 + c) * 4096, 0, kSc1);
+                };
+                load_block(0, x[0]);
+#pragma unroll
+                for (int i = 0; i < SM; ++i) {
+                    if (i + 1 < SM) load_block(i + 1, x[(i + 1) & 1]);
+#pragma unroll
+                    for (int j = 0; j < SN; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                acc[i][j][4 * q + e] = assign ? x[i & 1][j * 4 + q][e]
+                                                              : acc[i][j][4 * q + e] +
+                                                                    x[i & 1][j * 4 + q][e];
+                }
+            };
+            if (from_memory) add_partial(u1, true);
+            for (int u = from_memory ? u1 - 1 : u1; u >= u0; --u)
+                if (from_memory || u != unit) add_partial(u, false);
+        }
+
+        // -------------------------------------------------------- epilogue
+        uint16_t *tile = smem;
+        uint16_t *out = g.out + bt * g.sb_out;
+        const bool diag = (S != Stage::Apply) && (tm == tn);
+
+        if constexpr (S != Stage::Gram) {
+            // Epilogue operand tile (A for poly, X for apply) -> LDS, rows/cols outside
+            // the matrix read as zero.
+            const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
+            constexpr int kRowsPerInstr = 512 / BN;
+            constexpr int kLanesPerRow = BN / 8;
+#pragma unroll
+            for (int d = 0; d < Geo::kEpiLoads; ++d) {
+                const int blk = wave * Geo::kEpiLoads + d;
+                const int row = blk * kRowsPerInstr + lane / kLanesPerRow;
+                const int p = lane % kLanesPerRow;
+                const int c = p ^ ((row ^ (row >> 5)) & (kLanesPerRow - 1));
+                const int gr = row0 + row, gc = col0 + 8 * c;
+                const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
+                                       ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
+                                       : kOob;
+                dma_16B(rs_epi, smem_base + blk * 1024, v);
+            }
+            wait_vm_barrier<0>();
+        }
+
+        // Each lane turns its accumulators into bf16 results in place.
+#pragma unroll
+        for (int i = 0; i < SM; ++i) {
+            const int r = wr * WM + i * 32 + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < SN; ++j) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
+                    u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
+                    float e[4] = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (S != Stage::Gram) unpack4(*p, e);
+                    uint16_t h[4];
+                    epilogue_values<S>(acc[i][j], q, e, g, h);
+                    *p = pack4(h);
+                }
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+        // Coalesced store of the tile: 16-byte chunks, consecutive threads along a row.
+        constexpr int kChunksPerRow = BN / 8;
+        for (int idx = tid; idx < BM * kChunksPerRow; idx += 256) {
+            const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
+            const int gr = row0 + row, gc = col0 + 8 * c;
+            if constexpr (S == Stage::Apply) {
+                if (gr >= g.out_rows || gc >= g.out_cols) continue;
+            }
+            u32x4 v;
+            if (!diag) {
+                v = *reinterpret_cast<const u32x4 *>(tile + epi_offset<BN>(row, 8 * c));
+            } else {
+                // Diagonal tile: element (r, c) comes from the upper-triangle source
+                // min/max(r, c), so the stored matrix is bitwise symmetric.
                 uint32_t hh[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) hh[e] = tile[epi_offset<BN>(8 * rb + e, mc)];
-                const u32x4 v{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
-                              hh[6] | (hh[7] << 16)};
-                *reinterpret_cast<u32x4 *>(out + (col0 + mc) * g.ld_out + row0 + 8 * rb) = v;
+                for (int e = 0; e < 8; ++e) {
+                    const int col = 8 * c + e;
+                    hh[e] = row <= col ? tile[epi_offset<BN>(row, col)]
+                                       : tile[epi_offset<BN>(col, row)];
+                }
+                v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
+                          hh[6] | (hh[7] << 16)};
+            }
+            *reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc) = v;
+        }
+
+        // Mirrored store (symmetric stages, off-diagonal tiles): row c of the
+        // mirror tile is column c of this tile; consecutive threads walk along it.
+        if constexpr (S != Stage::Apply) {
+            if (!diag) {
+                constexpr int kMirrorChunks = BM / 8;  // 16-byte chunks per mirror row
+                for (int idx = tid; idx < BN * kMirrorChunks; idx += 256) {
+                    const int mc = idx / kMirrorChunks, rb = idx % kMirrorChunks;
+                    uint32_t hh[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) hh[e] = tile[epi_offset<BN>(8 * rb + e, mc)];
+                    const u32x4 v{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16),
+                                  hh[4] | (hh[5] << 16), hh[6] | (hh[7] << 16)};
+                    *reinterpret_cast<u32x4 *>(out + (col0 + mc) * g.ld_out + row0 + 8 * rb) = v;
+                }
             }
         }
     }
+}
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *p, int64_t n) {
+    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) p[i] = 0u;
 }
 
 template <int BM, int BN, Stage S>
@@ -369,10 +521,31 @@ hipError_t launch_stream_by_tile(int bm, int bn, const GemmArgs &g, int grid, hi
     return hipErrorInvalidValue;
 }
 
+template <int BM, int BN, Stage S>
+int occupancy_one() {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S>), 256, 0) != hipSuccess)
+        return 0;
+    return n;
+}
+
+template <Stage S>
+int occupancy_by_tile(int bm, int bn) {
+    if (bm == 64 && bn == 64) return occupancy_one<64, 64, S>();
+    if (bm == 128 && bn == 128) return occupancy_one<128, 128, S>();
+    if (bm == 256 && bn == 256) return occupancy_one<256, 256, S>();
+    if constexpr (S == Stage::Apply) {
+        if (bm == 128 && bn == 256) return occupancy_one<128, 256, S>();
+        if (bm == 256 && bn == 128) return occupancy_one<256, 128, S>();
+    }
+    return 0;
+}
+
 }  // namespace
 
 hipError_t launch_stream(Stage s, int bm, int bn, const GemmArgs &g, hipStream_t stream) {
-    const int grid = 8 * g.per_xcd;
+    const int grid = g.sk_units + 8 * g.per_xcd;
     switch (s) {
         case Stage::Gram:
             return launch_stream_by_tile<Stage::Gram>(bm, bn, g, grid, stream);
@@ -382,6 +555,27 @@ hipError_t launch_stream(Stage s, int bm, int bn, const GemmArgs &g, hipStream_t
             return launch_stream_by_tile<Stage::Apply>(bm, bn, g, grid, stream);
     }
     return hipErrorInvalidValue;
+}
+
+int stream_blocks_per_cu(Stage s, int bm, int bn) {
+    switch (s) {
+        case Stage::Gram:
+            return occupancy_by_tile<Stage::Gram>(bm, bn);
+        case Stage::Poly:
+            return occupancy_by_tile<Stage::Poly>(bm, bn);
+        case Stage::Apply:
+            return occupancy_by_tile<Stage::Apply>(bm, bn);
+    }
+    return 0;
+}
+
+hipError_t launch_zero_words(uint32_t *p, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    const int grid = static_cast<int>(blocks < 1024 ? blocks : 1024);
+    void *args[] = {&p, &n};
+    return hipLaunchKernel(reinterpret_cast<const void *>(&zero_words_kernel), dim3(grid), dim3(256),
+                           args, 0, stream);
 }
 
 }  // namespace muon_polar

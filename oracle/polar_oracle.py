@@ -27,6 +27,9 @@ What it restates (reference file:line):
 * ``pad_crop_step`` — the reference binding's pad-to-128/16 + crop semantics
   (``csrc/muon_polar_step_binding.cpp:630-672``), to show masking equals padding.
 * ``wrapper_step`` — the Python wrapper's M > N transpose policy (``muon_ascend950/ops.py:24-33``).
+* ``sparse_sign_input`` / ``polar_step_fused_sparse`` — ``polar_step_fused`` on sparse ±1
+  inputs whose sums are exact in fp32 in any order, so a kernel must match it bit for bit
+  at full size whatever its K split (no reference counterpart: a test device).
 
 How each function is pinned (``tests/test_oracle.py``): SVD closed form (one step maps
 singular values σ -> aσ + bσ³ + cσ⁵, five steps compose), textbook special cases of each
@@ -56,18 +59,25 @@ def f32_to_bf16_bits(x) -> np.ndarray:
     (a plain add could carry a NaN payload into infinity).
     """
     f = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
-    u = f.view(np.uint32).astype(np.uint64)
-    lsb = (u >> 16) & 1
-    rounded = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
+    u = f.view(np.uint32)
+    # u + 0x7FFF + lsb stays below 2^32 for every non-NaN pattern (the largest,
+    # -inf = 0xFF800000, gives 0xFF807FFF); NaN lanes are replaced below.
+    t = u >> 16
+    t &= 1
+    t += np.uint32(0x7FFF)
+    t += u
+    t >>= 16
+    rounded = t.astype(np.uint16)
     nan = np.isnan(f)
     if np.any(nan):
         rounded = np.where(nan, ((u >> 16).astype(np.uint16) | np.uint16(0x0040)), rounded)
-    return rounded.astype(np.uint16)
+    return rounded
 
 
 def bf16_bits_to_f32(bits) -> np.ndarray:
-    b = np.ascontiguousarray(np.asarray(bits, dtype=np.uint16))
-    return (b.astype(np.uint32) << 16).view(np.float32)
+    b = np.ascontiguousarray(np.asarray(bits, dtype=np.uint16)).astype(np.uint32)
+    b <<= 16
+    return b.view(np.float32)
 
 
 def bf16_round(x) -> np.ndarray:
@@ -167,6 +177,68 @@ def five_step_fused(x: np.ndarray, coefficients=COEFFICIENTS) -> np.ndarray:
     for a, b, c in coefficients:
         out = polar_step_fused(out, a, b, c)
     return out
+
+
+# ----------------------------------------------------------------------------- exact-sum inputs
+def sparse_sign_input(shape, nnz_per_row: int, seed: int = 0):
+    """Sparse X with entries in {-1, 0, +1}: ``nnz_per_row`` distinct random columns per
+    row, random signs.  Returns a list of scipy CSR matrices, one per batch matrix.
+
+    With such inputs (and small integer coefficients) every sum a kernel forms is an
+    integer far below 2^24, so its fp32 accumulation is exact in any order: split-K,
+    tile shape and summation order cannot change a single bit, and the kernel output
+    must equal ``polar_step_fused`` exactly.
+    """
+    import scipy.sparse as sp
+
+    *lead, m, n = shape
+    batch = int(np.prod(lead)) if lead else 1
+    rng = np.random.default_rng(seed)
+    mats = []
+    for _ in range(batch):
+        cols = np.argsort(rng.random((m, n)), axis=1)[:, :nnz_per_row] if n <= 4096 else \
+            np.stack([rng.choice(n, nnz_per_row, replace=False) for _ in range(m)])
+        vals = rng.choice(np.array([-1.0, 1.0]), size=(m, nnz_per_row))
+        rows = np.repeat(np.arange(m), nnz_per_row)
+        mats.append(sp.csr_matrix((vals.ravel(), (rows, cols.ravel())), shape=(m, n)))
+    return mats
+
+
+def _bf16_round_sparse(mat):
+    out = mat.tocsr(copy=True)
+    out.data = bf16_round(out.data).astype(np.float64)
+    out.eliminate_zeros()
+    return out
+
+
+def polar_step_fused_sparse(x_csr, a: float, b: float, c: float, return_stages: bool = False):
+    """``polar_step_fused`` for one sparse matrix (scipy CSR, float64 values).
+
+    Same rounding points (A = bf16(X·Xᵀ), P = bf16(b·A + c·A·A), Y = bf16(a·X + P·X),
+    coefficients rounded to fp32), exact float64 sums.  Returns (Y as a dense float64
+    array, max_sum), where max_sum bounds every partial sum a kernel accumulates (the sum
+    of |terms| of any output), so the caller can check that fp32 accumulation is exact
+    (max_sum < 2^24 with integer data).  With ``return_stages`` also A and P (dense).
+    """
+    a32, b32, c32 = (float(np.float32(v)) for v in (a, b, c))
+    x = x_csr.tocsr().astype(np.float64)
+    ax = abs(x)
+    gram = _bf16_round_sparse(x @ x.T)
+    ag = abs(gram)
+    poly = _bf16_round_sparse(b32 * gram + c32 * (gram @ gram)).toarray()
+    # P·X as (Xᵀ·Pᵀ)ᵀ: sparse times dense, cost nnz(X)·m; rounded in that
+    # (contiguous) transposed layout, transposed once at the end
+    yt = bf16_round(a32 * x.T.toarray() + x.T @ poly.T)
+    y = np.ascontiguousarray(yt.T).astype(np.float64)
+    max_col = np.diff(x.tocsc().indptr).max()
+    max_sum = max(
+        (ax @ ax.T).max(),
+        (ag @ ag).max() * abs(c32) + ag.max() * abs(b32),
+        np.abs(poly).max() * max_col + abs(a32),
+    )
+    if return_stages:
+        return y, float(max_sum), gram.toarray(), poly
+    return y, float(max_sum)
 
 
 # ----------------------------------------------------------------------------- boundary semantics

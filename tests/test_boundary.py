@@ -170,10 +170,15 @@ def test_entry_points_validate_before_launch():
     assert "workspace must hold" in capi.last_error()
     assert lib.muon_polar_step(16, 16, 16, 1, 1, 4, 8, 1.0, 1.0, 1.0, None) == capi.ERR_WORKSPACE
     assert lib.muon_polar_step(16, 16, 16, 1 << 20, 1, 8, 4, 1.0, 1.0, 1.0, None) == capi.ERR_INVALID_ARGUMENT
-    assert lib.muon_polar_gram(None, 16, 1, 4, 8, None) == capi.ERR_INVALID_ARGUMENT
-    assert lib.muon_polar_poly(16, None, 1, 4, 8, 1.0, 1.0, None) == capi.ERR_INVALID_ARGUMENT
-    assert lib.muon_polar_apply(16, 16, None, 1, 4, 8, 1.0, None) == capi.ERR_INVALID_ARGUMENT
-    assert lib.muon_polar_gram(16, 17, 1, 4, 8, None) == capi.ERR_INVALID_ARGUMENT  # misaligned
+    assert lib.muon_polar_gram(None, 16, None, 0, 1, 4, 8, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_poly(16, None, None, 0, 1, 4, 8, 1.0, 1.0, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_apply(16, 16, None, None, 0, 1, 4, 8, 1.0, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_gram(16, 17, None, 0, 1, 4, 8, None) == capi.ERR_INVALID_ARGUMENT  # misaligned
+    # an optional stage workspace, when given, is checked like polar_step's
+    assert lib.muon_polar_gram(16, 16, 16, 1, 1, 4, 8, None) == capi.ERR_WORKSPACE
+    assert lib.muon_polar_poly(16, 16, 16, 1, 1, 4, 8, 1.0, 1.0, None) == capi.ERR_WORKSPACE
+    assert lib.muon_polar_apply(16, 16, 16, 16, 1, 1, 4, 8, 1.0, None) == capi.ERR_WORKSPACE
+    assert lib.muon_polar_apply(16, 16, 16, 17, 1 << 20, 1, 4, 8, 1.0, None) == capi.ERR_WORKSPACE
 
 
 @pytest.mark.parametrize("var,value", [("MUON_POLAR_GRAM_TILE", "96"), ("MUON_POLAR_POLY_TILE", "512"),

@@ -229,3 +229,59 @@ def test_zero_output_fails_normwise_gate():
     # ... while the reference's elementwise 6e-2 gate alone accepts zeros here
     torch.testing.assert_close(torch.zeros(ref.shape, dtype=torch.float64),
                                torch.from_numpy(ref), rtol=6e-2, atol=6e-2)
+
+
+# ----------------------------------------------------------------------------- exact-sum inputs
+@pytest.mark.parametrize("shape,nnz", [((2, 96, 300), 5), ((1, 64, 640), 16), ((1, 33, 70), 3)])
+def test_sparse_fused_equals_dense_fused(shape, nnz):
+    """The sparse restatement gives the dense rounding-point emulation's bits, stages too."""
+    for xm in O.sparse_sign_input(shape, nnz, seed=4):
+        y, max_sum, a, p = O.polar_step_fused_sparse(xm, 2.0, -1.0, 1.0, return_stages=True)
+        yd, ad, pd = O.polar_step_fused(xm.toarray(), 2.0, -1.0, 1.0, return_stages=True)
+        assert np.array_equal(y, yd) and np.array_equal(a, ad) and np.array_equal(p, pd)
+        assert max_sum < 2**24
+
+
+def test_sparse_input_shape_and_values():
+    mats = O.sparse_sign_input((3, 40, 500), 7, seed=5)
+    assert len(mats) == 3
+    for xm in mats:
+        d = xm.toarray()
+        assert d.shape == (40, 500)
+        assert set(np.unique(d)) <= {-1.0, 0.0, 1.0}
+        assert (np.count_nonzero(d, axis=1) == 7).all()
+
+
+def test_exact_sums_are_order_independent():
+    """The premise of the bitwise split-K test: with these inputs the fp32 sum of any
+    K-split, in any order, is the exact sum (brute force over splits in float32)."""
+    xm = O.sparse_sign_input((1, 48, 1000), 16, seed=6)[0].toarray()
+    exact = xm @ xm.T
+    rng = np.random.default_rng(0)
+    for _ in range(5):
+        cuts = np.sort(rng.choice(np.arange(1, 1000), size=4, replace=False))
+        parts = [(xm[:, lo:hi] @ xm[:, lo:hi].T).astype(np.float32)
+                 for lo, hi in zip([0, *cuts], [*cuts, 1000])]
+        total = np.float32(0)
+        for part in rng.permutation(len(parts)):
+            total = total + parts[part]
+        assert np.array_equal(total.astype(np.float64), exact)
+
+
+def test_exact_sums_catch_a_dropped_or_doubled_k_range():
+    """Planted split-K mistakes (a 64-wide K range dropped, or counted twice, in the
+    gram stage) change Y's bits, so the bitwise GPU test would see them."""
+    xm = O.sparse_sign_input((1, 256, 4096), 16, seed=7)[0]
+    y_ok = O.polar_step_fused_sparse(xm, 2.0, -1.0, 1.0)[0]
+    d = xm.toarray()
+    for lo in (0, 1024, 4032):
+        dropped = d.copy()
+        dropped[:, lo:lo + 64] = 0.0
+        gram = O.bf16_round(dropped @ dropped.T).astype(np.float64)
+        poly = O.bf16_round(-gram + gram @ gram).astype(np.float64)
+        y_bad = O.bf16_round(2.0 * d + poly @ d)
+        assert not np.array_equal(y_bad, y_ok)
+        doubled = d @ d.T + d[:, lo:lo + 64] @ d[:, lo:lo + 64].T
+        gram = O.bf16_round(doubled).astype(np.float64)
+        poly = O.bf16_round(-gram + gram @ gram).astype(np.float64)
+        assert not np.array_equal(O.bf16_round(2.0 * d + poly @ d), y_ok)

@@ -215,13 +215,22 @@ def test_stages_against_oracle(shape):
     assert_within_dot_bound(yn, y_exact, abs(a32) * ax + np.abs(p[:, :m, :m]) @ ax)
     uy = O.bf16_ulp_distance(bits(y), O.f32_to_bf16_bits(y_exact.astype(np.float32)))
     assert (uy > 1).mean() < 5e-3
-    # whole step through the C ABI equals the torch op, bit for bit
+    # whole step through the C ABI equals the torch op, bit for bit, and the three
+    # stage calls given the same workspace (same stream-K split, if any); without
+    # a workspace the stages run unsplit, equal to fp32 rounding
     ws, _info = capi.alloc_workspace(batch, m, n)
     y2 = torch.empty_like(xd)
     capi.step(xd, y2, ws, a, b, c)
     y3 = polar_step(xd, a, b, c)
+    g_ws = torch.empty_like(gram)
+    p_ws = torch.empty_like(poly)
+    y4 = torch.empty_like(xd)
+    capi.gram(xd, g_ws, workspace=ws)
+    capi.poly(g_ws, p_ws, batch, m, n, b, c, workspace=ws)
+    capi.apply(p_ws, xd, y4, a, workspace=ws)
     torch.cuda.synchronize()
-    assert torch.equal(y, y2) and torch.equal(y2, y3)
+    assert torch.equal(y2, y3) and torch.equal(y2, y4)
+    assert_close_kernels(y, y2)
 
 
 def test_gram_special_cases():
@@ -276,7 +285,9 @@ def assert_close_kernels(a: torch.Tensor, b: torch.Tensor):
 def test_masking_equals_zero_padding(monkeypatch, shape):
     """Reference binding pads to 128/16 and crops (binding.cpp:630-672); masking must
     give the same numbers: bit for bit within one kernel family, to bf16 precision
-    when the padded shape switches to the DMA-fed kernels."""
+    when the padded shape switches to the DMA-fed kernels.  (Unsplit kernels: a
+    stream-K split depends on the tile count, which padding changes.)"""
+    monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
     x = O.make_input(shape, seed=7).to(DEV)
     batch, m, n = shape
     rows = -(-m // 128) * 128
@@ -330,8 +341,10 @@ def test_noncontiguous_input():
 ])
 def test_tile_configuration_does_not_change_results(monkeypatch, stream, env):
     """Every tile shape accumulates each output in the same K order, so results are
-    bit-identical across tile configurations of one kernel family."""
+    bit-identical across tile configurations of one kernel family (unsplit: a
+    stream-K split cuts K where the tile count puts it)."""
     monkeypatch.setenv("MUON_POLAR_STREAM", stream)
+    monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
     x = O.make_input((2, 300, 1000), seed=11).to(DEV)
     base = polar_step(x, *C0)
     for k, v in env.items():
