@@ -174,7 +174,7 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
         for (int i = 0; i < Geo::kLoadsB; ++i) {
             if constexpr (S == Stage::Apply) {
                 const int krow = b_krow(i);
-                const int c = (lane % kBLanesPerRow) ^ ((krow & 3) << 1);
+                const int c = (lane % kBLanesPerRow) ^ nc_swz<BN>(krow);
                 const int col = col0 + 8 * c;
                 off_b[i] =
                     col < g.col_rows ? static_cast<uint32_t>((krow * g.ld_col + col) * 2) : kOob;

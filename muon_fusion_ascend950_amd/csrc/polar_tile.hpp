@@ -61,12 +61,20 @@ __device__ __forceinline__ int kc_offset(int row, int chunk) {
 }
 
 // N-contiguous tile [64][BN] (stage-3 X panel, rows = K): chunk c of K-row k is
-// stored at c ^ (2*(k%4)).  A transposing read fetches 4 consecutive K-rows by
-// 2 chunks (32 B) per 16-lane group; the XOR spreads those 8 chunks over 8
-// distinct bank groups.
+// stored at c ^ nc_swz(k).  A transposing read fetches 4 consecutive K-rows by
+// 2 chunks (32 B) per 16-lane group, and a half-wave (two groups: 16 adjacent
+// columns each) is served per LDS cycle.  Rows are 2*BN bytes apart, a multiple
+// of the 256-byte bank window, so without the XOR all 4 rows would share banks.
+// XOR by 4*(k%4) (BN >= 128) puts the half-wave's 16 chunks on 16 distinct
+// positions of the window: no bank conflict.  BN = 64 rows have 8 chunks only;
+// XOR by 2*(k%4) there (two groups then share banks).
+template <int BN>
+__device__ __forceinline__ int nc_swz(int krow) {
+    return BN >= 128 ? (krow & 3) << 2 : (krow & 3) << 1;
+}
 template <int BN>
 __device__ __forceinline__ int nc_offset(int krow, int chunk) {
-    return krow * BN + ((chunk ^ ((krow & 3) << 1)) << 3);
+    return krow * BN + ((chunk ^ nc_swz<BN>(krow)) << 3);
 }
 
 // ---------------------------------------------------------------------------
