@@ -17,6 +17,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <numeric>
 #include <string>
 #include <unordered_map>
 
@@ -97,6 +98,7 @@ struct SkSplit {
 };
 
 struct Plan {
+    int64_t m;   // rows of X
     int64_t mp;  // padded extent / leading dimension of A and P
     int gram_tile, poly_tile, apply_bm, apply_bn;
     int gram_nt, poly_nt;           // tiles per side of the triangular stages
@@ -116,10 +118,17 @@ struct Plan {
 std::mutex g_plan_mutex;
 std::unordered_map<PlanKey, Plan, PlanKeyHash> g_plans;
 
-// Default tile shape by matrix size: large tiles keep the MFMA pipes fed
-// (LDS traffic per flop falls with the tile edge); small matrices need smaller
-// tiles to put enough workgroups on the 256 CUs.
+// Default tile shapes by matrix size (measured on MI355X).  Stage 3 keeps the
+// MFMA pipes fed best with 256x256 tiles once there are enough of them (m >=
+// 2048).  The triangular stages run 128x128 tiles: two workgroups share a CU
+// and hide each other's memory and barrier waits, which beats 256x256 tiles
+// (one per CU) at every size measured, by 2x at m = 2048.  Small matrices use
+// 64x64 tiles to put enough workgroups on the 256 CUs.
 uint32_t default_square_tile(int64_t m) {
+    if (m > 256) return 128;
+    return 64;
+}
+uint32_t default_apply_tile(int64_t m) {
     if (m >= 2048) return 256;
     if (m > 256) return 128;
     return 64;
@@ -130,16 +139,16 @@ int read_knobs(int64_t m, int64_t n, Knobs &k) {
     const uint32_t def = default_square_tile(m);
     k.gram_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_TILE", def));
     k.poly_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_POLY_TILE", k.gram_tile));
-    k.apply_bm = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_M", def));
+    k.apply_bm = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_M", default_apply_tile(m)));
     k.apply_bn = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_N", k.apply_bm));
     k.stream = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM", 1));
     if (k.stream > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM must be 0 or 1");
     k.stream_k = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM_K", 1));
     if (k.stream_k > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM_K must be 0 or 1");
     if (!muon_polar::tile_supported(Stage::Gram, k.gram_tile, k.gram_tile))
-        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE must be 64, 128 or 256");
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE must be 64, 128, 192 or 256");
     if (!muon_polar::tile_supported(Stage::Poly, k.poly_tile, k.poly_tile))
-        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_POLY_TILE must be 64, 128 or 256");
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_POLY_TILE must be 64, 128, 192 or 256");
     if (!muon_polar::tile_supported(Stage::Apply, k.apply_bm, k.apply_bn))
         return fail(MUON_POLAR_ERR_CONFIG,
                     "MUON_POLAR_APPLY_TILE_M/_N must be 64x64, 128x128, 256x256, 128x256 or "
@@ -211,7 +220,11 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.poly_tile = static_cast<int>(knobs.poly_tile);
     p.apply_bm = static_cast<int>(knobs.apply_bm);
     p.apply_bn = static_cast<int>(knobs.apply_bn);
-    p.mp = round_up(m, std::max(p.gram_tile, p.poly_tile));
+    p.m = m;
+    // A and P are tiled by both stage tiles: pad to a common multiple.
+    p.mp = round_up(m, std::lcm(p.gram_tile, p.poly_tile));
+    if (p.mp * p.mp >= (int64_t(1) << 30))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "matrix too large (2^30 elements or more)");
     p.gram_nt = static_cast<int>(p.mp / p.gram_tile);
     p.poly_nt = static_cast<int>(p.mp / p.poly_tile);
     p.apply_tm = static_cast<int>((m + p.apply_bm - 1) / p.apply_bm);
@@ -235,7 +248,7 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     const int tiles_bn[3] = {p.gram_tile, p.poly_tile, p.apply_bn};
     const Stage stages[3] = {Stage::Gram, Stage::Poly, Stage::Apply};
     const int64_t grids[3] = {p.gram_grid, p.poly_grid, p.apply_grid};
-    const int64_t ksteps[3] = {round_up(n, 64) / 64, p.mp / 64, p.mp / 64};
+    const int64_t ksteps[3] = {round_up(n, 64) / 64, round_up(m, 64) / 64, round_up(m, 64) / 64};
     p.sk_any = false;
     p.counter_stride = 0;
     size_t partial_bytes = 0;
@@ -368,7 +381,8 @@ int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double 
     g.sb_row = g.sb_col = g.sb_epi = g.sb_out = p.mp * p.mp;
     g.ld_row = g.ld_col = g.ld_epi = g.ld_out = static_cast<int32_t>(p.mp);
     g.row_rows = g.col_rows = g.row_k = g.col_k = static_cast<int32_t>(p.mp);
-    g.k_loop = static_cast<int32_t>(p.mp);
+    // A is zero beyond row / column m: the K loop stops at m (rounded to a step).
+    g.k_loop = static_cast<int32_t>(round_up(p.m, 64));
     g.out_rows = g.out_cols = static_cast<int32_t>(p.mp);
     g.tiles_m = g.tiles_n = p.poly_nt;
     g.tiles_per_batch = p.poly_nt * (p.poly_nt + 1) / 2;
@@ -393,7 +407,7 @@ int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t b
     g.row_rows = g.row_k = static_cast<int32_t>(p.mp);
     g.col_rows = static_cast<int32_t>(n);
     g.col_k = static_cast<int32_t>(m);
-    g.k_loop = static_cast<int32_t>(p.mp);
+    g.k_loop = static_cast<int32_t>(round_up(m, 64));  // P is zero beyond column m
     g.out_rows = static_cast<int32_t>(m);
     g.out_cols = static_cast<int32_t>(n);
     g.tiles_m = p.apply_tm;

@@ -132,6 +132,9 @@ hipError_t launch_by_tile(int bm, int bn, const GemmArgs &g, int grid, hipStream
     if (bm == 64 && bn == 64) return launch_one<64, 64, S, VEC>(g, grid, stream);
     if (bm == 128 && bn == 128) return launch_one<128, 128, S, VEC>(g, grid, stream);
     if (bm == 256 && bn == 256) return launch_one<256, 256, S, VEC>(g, grid, stream);
+    if constexpr (S != Stage::Apply) {
+        if (bm == 192 && bn == 192) return launch_one<192, 192, S, VEC>(g, grid, stream);
+    }
     if constexpr (S == Stage::Apply) {
         if (bm == 128 && bn == 256) return launch_one<128, 256, S, VEC>(g, grid, stream);
         if (bm == 256 && bn == 128) return launch_one<256, 128, S, VEC>(g, grid, stream);
@@ -143,6 +146,7 @@ hipError_t launch_by_tile(int bm, int bn, const GemmArgs &g, int grid, hipStream
 
 bool tile_supported(Stage s, int bm, int bn) {
     if (bm == bn && (bm == 64 || bm == 128 || bm == 256)) return true;
+    if (s != Stage::Apply && bm == 192 && bn == 192) return true;
     if (s == Stage::Apply && ((bm == 128 && bn == 256) || (bm == 256 && bn == 128))) return true;
     return false;
 }

@@ -30,13 +30,15 @@ namespace muon_polar {
 
 namespace {
 
-constexpr int kStages = 2;
-
 template <int BM, int BN>
 struct StreamGeom {
     static constexpr int kABytes = BM * kBK * 2;        // row-operand panel per K-step
     static constexpr int kBBytes = BN * kBK * 2;        // col-operand panel per K-step
     static constexpr int kStageBytes = kABytes + kBBytes;
+    // Ring depth.  A third slot (where it fits in LDS) measured slower on every
+    // tile shape: more DMA in flight competes with the fragment reads; the
+    // loop below is written for either depth.
+    static constexpr int kStages = 2;
     static constexpr int kLoadsA = kABytes / 1024 / 4;  // DMA instructions per wave
     static constexpr int kLoadsB = kBBytes / 1024 / 4;
     static constexpr int kLoads = kLoadsA + kLoadsB;
@@ -44,16 +46,25 @@ struct StreamGeom {
     static constexpr int kEpiLoads = kTileBytes / 1024 / 4;
     static_assert(kLoadsA >= 1 && kLoadsB >= 1, "tile too small for 4 waves");
     static_assert(kTileBytes <= kStages * kStageBytes, "epilogue tile must fit the ring");
+    static_assert(kTileBytes % 4096 == 0, "epilogue DMA is whole 1 KiB blocks per wave");
 };
 
-// Epilogue tile in LDS: [BM][BN] bf16, 16-byte chunk c of row r stored at chunk
-// position c ^ ((r ^ (r >> 5)) & (BN/8 - 1)).  32 consecutive rows at one chunk
-// (MFMA-layout accesses) and 32 rows spaced 8 apart (mirror reads) both land on
-// distinct chunk positions.
+// Epilogue tile in LDS: [BM][BN] bf16.  BN a power of two: 16-byte chunk c of
+// row r is stored at chunk position c ^ ((r ^ (r >> 5)) & (BN/8 - 1)), so 32
+// consecutive rows at one chunk (MFMA-layout accesses) and 32 rows spaced 8
+// apart (mirror reads) land on distinct positions.  BN = 192 (24 chunks): the
+// XOR acts within each group of 8 chunks.  Either way the map is its own
+// inverse for a fixed row.
+template <int BN>
+__device__ __forceinline__ int epi_pos(int row, int chunk) {
+    if constexpr ((BN & (BN - 1)) == 0)
+        return chunk ^ ((row ^ (row >> 5)) & (BN / 8 - 1));
+    else
+        return (chunk & ~7) | ((chunk ^ (row ^ (row >> 3))) & 7);
+}
 template <int BN>
 __device__ __forceinline__ int epi_offset(int row, int col) {
-    constexpr int kMask = BN / 8 - 1;
-    return row * BN + ((((col >> 3) ^ ((row ^ (row >> 5)) & kMask))) << 3) + (col & 7);
+    return row * BN + (epi_pos<BN>(row, col >> 3) << 3) + (col & 7);
 }
 
 // Stream-K bookkeeping (all values uniform across the workgroup).
@@ -80,6 +91,7 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
     constexpr int kMfmaPerSlice = SM * SN;
     static_assert(S == Stage::Apply || BM == BN, "triangular stages need square tiles");
 
+    constexpr int kStages = Geo::kStages;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * Geo::kStageBytes / 2];
     __shared__ uint32_t s_arrived;
 
@@ -276,22 +288,33 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
         };
         static_assert(kBK / 16 == 4, "schedule below is written for four k16 slices per step");
 
-        // Schedule per K-step k (slot k%2), slices s0..s3 of 16 K-values:
+        // Schedule per K-step k (slot k % kStages), slices s0..s3 of 16 K-values:
         //   frags(s1) | mfma(s0) | frags(s2) | mfma(s1) | frags(s3) | mfma(s2) |
-        //   wait panel k+1, barrier | frags(next s0) | mfma(s3) + DMA panel k+2 -> slot k%2
-        // The barrier sits where every wave has read all of slot k%2 into registers.
+        //   wait panel k+1, barrier | frags(next s0) | mfma(s3) + DMA panel k+kStages -> slot
+        // The barrier sits where every wave has read all of step k's slot into
+        // registers; panels k+2 .. k+kStages-1 may still be in flight there.
         const int nkl = kend - kbeg;
         bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
         issue_all(kbeg, 0);
-        if (nkl > 1) {
-            issue_all(kbeg + 1, 1);
-            wait_vm_barrier<Geo::kLoads>();
+        if (nkl > 1) issue_all(kbeg + 1, 1);
+        if constexpr (kStages == 3) {
+            if (nkl > 2) issue_all(kbeg + 2, 2);
+            if (nkl > 2)
+                wait_vm_barrier<2 * Geo::kLoads>();
+            else if (nkl > 1)
+                wait_vm_barrier<Geo::kLoads>();
+            else
+                wait_vm_barrier<0>();
         } else {
-            wait_vm_barrier<0>();
+            if (nkl > 1)
+                wait_vm_barrier<Geo::kLoads>();
+            else
+                wait_vm_barrier<0>();
         }
         load_frags(0, 0, fr0, fc0);
+        int slot = 0;
         for (int k = 0; k < nkl; ++k) {
-            const int slot = k & 1;
+            const int next = slot + 1 == kStages ? 0 : slot + 1;
             load_frags(slot, 1, fr1, fc1);
             __builtin_amdgcn_sched_barrier(0);
             mfmas(fr0, fc0);
@@ -305,13 +328,18 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
             mfmas(fr0, fc0);
             __builtin_amdgcn_sched_barrier(0);
             if (k + 1 < nkl) {
-                wait_vm_barrier<0>();
-                load_frags(slot ^ 1, 0, fr0, fc0);
+                if (kStages == 3 && k + 2 < nkl)
+                    wait_vm_barrier<Geo::kLoads>();  // panel k+2 may stay in flight
+                else
+                    wait_vm_barrier<0>();
+                load_frags(next, 0, fr0, fc0);
             }
             __builtin_amdgcn_sched_barrier(0);
-            const bool more = k + 2 < nkl;
-            mfmas_with_dma(fr1, fc1, kbeg + k + 2, slot, more, more && is_tail(kbeg + k + 2));
+            const bool more = k + kStages < nkl;
+            mfmas_with_dma(fr1, fc1, kbeg + k + kStages, slot, more,
+                           more && is_tail(kbeg + k + kStages));
             __builtin_amdgcn_sched_barrier(0);
+            slot = next;
         }
         // All waves are done with the ring (and no DMA is outstanding).
         wait_vm_barrier<0>();
@@ -414,14 +442,15 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
             // Epilogue operand tile (A for poly, X for apply) -> LDS, rows/cols outside
             // the matrix read as zero.
             const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
-            constexpr int kRowsPerInstr = 512 / BN;
-            constexpr int kLanesPerRow = BN / 8;
+            constexpr int kChunksPerRow = BN / 8;
 #pragma unroll
             for (int d = 0; d < Geo::kEpiLoads; ++d) {
+                // LDS chunk q of the tile (row q / kChunksPerRow, position q %
+                // kChunksPerRow) receives global chunk epi_pos(row, position).
                 const int blk = wave * Geo::kEpiLoads + d;
-                const int row = blk * kRowsPerInstr + lane / kLanesPerRow;
-                const int p = lane % kLanesPerRow;
-                const int c = p ^ ((row ^ (row >> 5)) & (kLanesPerRow - 1));
+                const int q = blk * 64 + lane;
+                const int row = q / kChunksPerRow;
+                const int c = epi_pos<BN>(row, q - row * kChunksPerRow);
                 const int gr = row0 + row, gc = col0 + 8 * c;
                 const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
                                        ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
@@ -514,6 +543,9 @@ hipError_t launch_stream_by_tile(int bm, int bn, const GemmArgs &g, int grid, hi
     if (bm == 64 && bn == 64) return launch_stream_one<64, 64, S>(g, grid, stream);
     if (bm == 128 && bn == 128) return launch_stream_one<128, 128, S>(g, grid, stream);
     if (bm == 256 && bn == 256) return launch_stream_one<256, 256, S>(g, grid, stream);
+    if constexpr (S != Stage::Apply) {
+        if (bm == 192 && bn == 192) return launch_stream_one<192, 192, S>(g, grid, stream);
+    }
     if constexpr (S == Stage::Apply) {
         if (bm == 128 && bn == 256) return launch_stream_one<128, 256, S>(g, grid, stream);
         if (bm == 256 && bn == 128) return launch_stream_one<256, 128, S>(g, grid, stream);
@@ -535,6 +567,9 @@ int occupancy_by_tile(int bm, int bn) {
     if (bm == 64 && bn == 64) return occupancy_one<64, 64, S>();
     if (bm == 128 && bn == 128) return occupancy_one<128, 128, S>();
     if (bm == 256 && bn == 256) return occupancy_one<256, 256, S>();
+    if constexpr (S != Stage::Apply) {
+        if (bm == 192 && bn == 192) return occupancy_one<192, 192, S>();
+    }
     if constexpr (S == Stage::Apply) {
         if (bm == 128 && bn == 256) return occupancy_one<128, 256, S>();
         if (bm == 256 && bn == 128) return occupancy_one<256, 128, S>();

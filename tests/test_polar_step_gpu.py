@@ -338,6 +338,10 @@ def test_noncontiguous_input():
     {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_POLY_TILE": "128", "MUON_POLAR_APPLY_TILE_M": "256",
      "MUON_POLAR_APPLY_TILE_N": "128"},
     {"MUON_POLAR_APPLY_TILE_M": "128", "MUON_POLAR_APPLY_TILE_N": "256"},
+    {"MUON_POLAR_GRAM_TILE": "192", "MUON_POLAR_POLY_TILE": "192"},
+    {"MUON_POLAR_GRAM_TILE": "192", "MUON_POLAR_POLY_TILE": "256"},
+    {"MUON_POLAR_GRAM_TILE": "128", "MUON_POLAR_POLY_TILE": "192", "MUON_POLAR_APPLY_TILE_M": "256",
+     "MUON_POLAR_APPLY_TILE_N": "128"},
 ])
 def test_tile_configuration_does_not_change_results(monkeypatch, stream, env):
     """Every tile shape accumulates each output in the same K order, so results are

@@ -31,7 +31,9 @@ EXACT_COEFFS = (2.0, -1.0, 1.0)
 # (batch, m, n): headline shape (all three stages split), batch crossing inside the
 # split range, ragged m and n (padded rows, partial last K-step, edge column tiles),
 # 128-row tiles.
-SPLIT_SHAPES = [(1, 4096, 14336), (3, 2048, 4096), (1, 2000, 4040), (1, 1024, 8192)]
+SPLIT_SHAPES = [(1, 4096, 14336), (3, 1024, 8192), (1, 2000, 4040), (1, 1024, 8192)]
+# the same with 256x256 tiles for the triangular stages (256 KiB partials)
+BIG_TILES = {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_POLY_TILE": "256"}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -72,9 +74,14 @@ def test_split_is_in_use(shape):
 
 
 @pytest.mark.parametrize("split", ["1", "0"])
-@pytest.mark.parametrize("shape", SPLIT_SHAPES)
-def test_exact_sums_are_bitwise(monkeypatch, shape, split):
+@pytest.mark.parametrize("shape,env", [(s, {}) for s in SPLIT_SHAPES] +
+                         [((1, 4096, 14336), BIG_TILES), ((2, 2048, 4096), BIG_TILES)])
+def test_exact_sums_are_bitwise(monkeypatch, shape, env, split):
     monkeypatch.setenv("MUON_POLAR_STREAM_K", split)
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    if split == "1":
+        assert split_in_use(*shape)
     capi = _capi()
     batch, m, n = shape
     mats = O.sparse_sign_input(shape, 16, seed=21)
@@ -103,7 +110,7 @@ def test_exact_sums_are_bitwise(monkeypatch, shape, split):
         assert_bits_equal(bits(y[i]), O.f32_to_bf16_bits(y_ref.astype(np.float32)), "Y")
 
 
-@pytest.mark.parametrize("shape", [(1, 4096, 14336), (3, 2048, 4096), (1, 1024, 8192)])
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (3, 1024, 8192), (1, 1024, 8192)])
 def test_split_agrees_with_unsplit_and_is_deterministic(monkeypatch, shape):
     x = O.make_input(shape, seed=22).to(DEV)
     first = polar_step(x, *C0)
