@@ -54,9 +54,11 @@ struct Knobs {
     uint32_t gram_tile, poly_tile, apply_bm, apply_bn;
     uint32_t stream;    // 1: DMA-fed kernels where eligible; 0: register-staged kernels only
     uint32_t stream_k;  // 1: stream-K split of a partial last round (polar_step only); 0: off
+    uint32_t waves;     // waves per workgroup of the 256x256 DMA-fed kernels (4 or 8)
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
-               apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k;
+               apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k &&
+               waves == o.waves;
     }
 };
 
@@ -85,6 +87,7 @@ struct PlanKeyHash {
         mix(static_cast<uint64_t>(k.knobs.apply_bm) << 32 | k.knobs.apply_bn);
         mix(k.knobs.stream);
         mix(k.knobs.stream_k);
+        mix(k.knobs.waves);
         return static_cast<size_t>(h);
     }
 };
@@ -106,6 +109,7 @@ struct Plan {
     int64_t gram_grid, poly_grid, apply_grid;
     size_t gram_bytes, workspace_bytes;
     bool stream;
+    int waves[3];  // waves per workgroup of the DMA-fed kernel of each stage
     // polar_step's stream-K splits (gram, poly, apply) and their workspace areas
     // after A and P: arrival counters (counter_stride words per stage), then
     // the fp32 partial slots shared by the three stages.
@@ -118,18 +122,23 @@ struct Plan {
 std::mutex g_plan_mutex;
 std::unordered_map<PlanKey, Plan, PlanKeyHash> g_plans;
 
-// Default tile shapes by matrix size (measured on MI355X).  Stage 3 keeps the
-// MFMA pipes fed best with 256x256 tiles once there are enough of them (m >=
-// 2048).  The triangular stages run 128x128 tiles: two workgroups share a CU
-// and hide each other's memory and barrier waits, which beats 256x256 tiles
-// (one per CU) at every size measured, by 2x at m = 2048.  Small matrices use
-// 64x64 tiles to put enough workgroups on the 256 CUs.
+// Default tile shapes by matrix size (measured on MI355X).  256x256 tiles run
+// with 8 waves (two per SIMD: one wave's LDS and barrier waits are covered by
+// the other's MFMAs), 12% faster per step than 4 waves at 4096 x 14336.  The
+// triangular stages use them from m = 4096; below that, 128x128 tiles (two
+// workgroups per CU) are faster there (2x at m = 2048, where a 256x256 grid
+// has too few tiles).  Stage 3 has 4x more tiles and prefers 256x256 from
+// m = 1024.  Small matrices use 64x64 tiles to put enough workgroups on the
+// 256 CUs.
+constexpr uint32_t kDefaultWaves = 8;
+
 uint32_t default_square_tile(int64_t m) {
+    if (m >= 4096) return 256;
     if (m > 256) return 128;
     return 64;
 }
 uint32_t default_apply_tile(int64_t m) {
-    if (m >= 2048) return 256;
+    if (m >= 1024) return 256;
     if (m > 256) return 128;
     return 64;
 }
@@ -145,6 +154,9 @@ int read_knobs(int64_t m, int64_t n, Knobs &k) {
     if (k.stream > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM must be 0 or 1");
     k.stream_k = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM_K", 1));
     if (k.stream_k > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM_K must be 0 or 1");
+    k.waves = static_cast<uint32_t>(env_u64("MUON_POLAR_WAVES", kDefaultWaves));
+    if (k.waves != 4 && k.waves != 8)
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_WAVES must be 4 or 8");
     if (!muon_polar::tile_supported(Stage::Gram, k.gram_tile, k.gram_tile))
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE must be 64, 128, 192 or 256");
     if (!muon_polar::tile_supported(Stage::Poly, k.poly_tile, k.poly_tile))
@@ -252,9 +264,12 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.sk_any = false;
     p.counter_stride = 0;
     size_t partial_bytes = 0;
+    for (int s = 0; s < 3; ++s)
+        p.waves[s] = muon_polar::stream_waves(tiles_bm[s], tiles_bn[s], static_cast<int>(knobs.waves));
     for (int s = 0; s < 3; ++s) {
-        const int occ =
-            sk_ok ? muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s], tiles_bn[s]) : 0;
+        const int occ = sk_ok ? muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s],
+                                                                 tiles_bn[s], p.waves[s])
+                              : 0;
         p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ,
                             sk_min_share(tiles_bm[s], tiles_bn[s]));
         if (p.sk[s].sk_units > 0) {
@@ -298,9 +313,9 @@ struct SkArea {
 };
 
 // Launch one stage: DMA-fed kernel when allowed, register-staged otherwise.
-hipError_t launch_stage(Stage s, int bm, int bn, bool stream_ok, bool vec, GemmArgs &g,
-                        int64_t batch, int64_t grid, const SkSplit *sk, const SkArea *area,
-                        hipStream_t stream) {
+hipError_t launch_stage(Stage s, int bm, int bn, int waves, bool stream_ok, bool vec,
+                        GemmArgs &g, int64_t batch, int64_t grid, const SkSplit *sk,
+                        const SkArea *area, hipStream_t stream) {
     g.total_tiles = static_cast<int32_t>(batch * g.tiles_per_batch);
     g.k_steps = g.k_loop / 64;
     g.dp_tiles = g.total_tiles;
@@ -314,7 +329,7 @@ hipError_t launch_stage(Stage s, int bm, int bn, bool stream_ok, bool vec, GemmA
         g.counters = area->counters;
     }
     g.per_xcd = (g.dp_tiles + 7) / 8;
-    if (stream_ok) return muon_polar::launch_stream(s, bm, bn, g, stream);
+    if (stream_ok) return muon_polar::launch_stream(s, bm, bn, waves, g, stream);
     return muon_polar::launch_gemm(s, bm, bn, vec, g, static_cast<int>(grid), stream);
 }
 
@@ -368,7 +383,8 @@ int run_gram(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m,
     g.s_acc = 1.0f;
     g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
     const bool vec = (n % 8 == 0) && aligned16(x);
-    return finish_stage(launch_stage(Stage::Gram, p.gram_tile, p.gram_tile, p.stream && vec, vec,
+    return finish_stage(launch_stage(Stage::Gram, p.gram_tile, p.gram_tile, p.waves[0],
+                                     p.stream && vec, vec,
                                      g, batch, p.gram_grid, &p.sk[0], area, stream),
                         stream, "gram");
 }
@@ -389,7 +405,8 @@ int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double 
     g.s_epi = static_cast<float>(b);
     g.s_acc = static_cast<float>(c);
     g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(p.mp * p.mp * 2);
-    return finish_stage(launch_stage(Stage::Poly, p.poly_tile, p.poly_tile, p.stream, true, g,
+    return finish_stage(launch_stage(Stage::Poly, p.poly_tile, p.poly_tile, p.waves[1], p.stream,
+                                     true, g,
                                      batch, p.poly_grid, &p.sk[1], area, stream),
                         stream, "poly");
 }
@@ -419,7 +436,8 @@ int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t b
     g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
     g.group_n = static_cast<int32_t>(std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", 8)));
     const bool vec = (n % 8 == 0) && aligned16(x) && aligned16(y);
-    return finish_stage(launch_stage(Stage::Apply, p.apply_bm, p.apply_bn, p.stream && vec, vec,
+    return finish_stage(launch_stage(Stage::Apply, p.apply_bm, p.apply_bn, p.waves[2],
+                                     p.stream && vec, vec,
                                      g, batch, p.apply_grid, &p.sk[2], area, stream),
                         stream, "apply");
 }

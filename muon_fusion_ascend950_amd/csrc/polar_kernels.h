@@ -52,11 +52,17 @@ hipError_t launch_gemm(Stage s, int bm, int bn, bool vec, const GemmArgs &g, int
                        hipStream_t stream);
 
 // DMA-fed kernels: X chunks of 16 B must be entirely inside or outside the matrix
-// (n % 8 == 0, 16-byte aligned X).  Grid is g.sk_units + 8 * g.per_xcd.
-hipError_t launch_stream(Stage s, int bm, int bn, const GemmArgs &g, hipStream_t stream);
+// (n % 8 == 0, 16-byte aligned X).  Grid is g.sk_units + 8 * g.per_xcd; `waves`
+// per workgroup as returned by stream_waves.
+hipError_t launch_stream(Stage s, int bm, int bn, int waves, const GemmArgs &g,
+                         hipStream_t stream);
 
-// Workgroups of the DMA-fed kernel for (s, bm, bn) resident per CU (0 on error).
-int stream_blocks_per_cu(Stage s, int bm, int bn);
+// Waves per workgroup the DMA-fed kernel of a bm x bn tile runs with, given the
+// requested count (8 is available for 256x256 tiles; 4 otherwise).
+int stream_waves(int bm, int bn, int requested);
+
+// Workgroups of the DMA-fed kernel for (s, bm, bn, waves) resident per CU (0 on error).
+int stream_blocks_per_cu(Stage s, int bm, int bn, int waves);
 
 // Sets n 32-bit words at p to zero (stream-ordered, no memset node).
 hipError_t launch_zero_words(uint32_t *p, int64_t n, hipStream_t stream);

@@ -30,8 +30,13 @@ namespace muon_polar {
 
 namespace {
 
-template <int BM, int BN>
+// NW waves per workgroup in a 2 x NW/2 grid over the tile: 4 (one wave per
+// SIMD, 128x128 wave tiles for a 256x256 tile) or 8 (two waves per SIMD, 128x64
+// wave tiles: 1.5x the fragment reads, but one wave's LDS and barrier waits are
+// covered by the other's MFMAs).
+template <int BM, int BN, int NW>
 struct StreamGeom {
+    static constexpr int kThreads = 64 * NW;
     static constexpr int kABytes = BM * kBK * 2;        // row-operand panel per K-step
     static constexpr int kBBytes = BN * kBK * 2;        // col-operand panel per K-step
     static constexpr int kStageBytes = kABytes + kBBytes;
@@ -39,14 +44,16 @@ struct StreamGeom {
     // tile shape: more DMA in flight competes with the fragment reads; the
     // loop below is written for either depth.
     static constexpr int kStages = 2;
-    static constexpr int kLoadsA = kABytes / 1024 / 4;  // DMA instructions per wave
-    static constexpr int kLoadsB = kBBytes / 1024 / 4;
+    static constexpr int kLoadsA = kABytes / 1024 / NW;  // DMA instructions per wave
+    static constexpr int kLoadsB = kBBytes / 1024 / NW;
     static constexpr int kLoads = kLoadsA + kLoadsB;
-    static constexpr int kTileBytes = BM * BN * 2;      // bf16 output tile (epilogue)
-    static constexpr int kEpiLoads = kTileBytes / 1024 / 4;
-    static_assert(kLoadsA >= 1 && kLoadsB >= 1, "tile too small for 4 waves");
+    static constexpr int kTileBytes = BM * BN * 2;       // bf16 output tile (epilogue)
+    static constexpr int kEpiLoads = kTileBytes / 1024 / NW;
+    static_assert(kLoadsA >= 1 && kLoadsB >= 1 && kABytes % (1024 * NW) == 0 &&
+                      kBBytes % (1024 * NW) == 0,
+                  "panels must split into whole 1 KiB DMA blocks per wave");
     static_assert(kTileBytes <= kStages * kStageBytes, "epilogue tile must fit the ring");
-    static_assert(kTileBytes % 4096 == 0, "epilogue DMA is whole 1 KiB blocks per wave");
+    static_assert(kTileBytes % (1024 * NW) == 0, "epilogue DMA is whole 1 KiB blocks per wave");
 };
 
 // Epilogue tile in LDS: [BM][BN] bf16.  BN a power of two: 16-byte chunk c of
@@ -83,10 +90,11 @@ __device__ __forceinline__ int sk_slot(const GemmArgs &g, int u, int st) {
     return 2 * u + (st != static_cast<int>(sk_bound(g, u) / g.k_steps));
 }
 
-template <int BM, int BN, Stage S>
-__global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
-    using Geo = StreamGeom<BM, BN>;
-    constexpr int WM = BM / 2, WN = BN / 2;
+template <int BM, int BN, Stage S, int NW>
+__global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
+    using Geo = StreamGeom<BM, BN, NW>;
+    constexpr int kThreads = Geo::kThreads;
+    constexpr int WM = BM / 2, WN = BN / (NW / 2);
     constexpr int SM = WM / 32, SN = WN / 32;
     constexpr int kMfmaPerSlice = SM * SN;
     static_assert(S == Stage::Apply || BM == BN, "triangular stages need square tiles");
@@ -367,7 +375,8 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
                 return static_cast<uint32_t>(int64_t(sk_slot(g, u, lt)) * slot_bytes) + tid * 16;
             };
             // Slot layout: 16-byte chunk c = (i * SN + j) * 4 + q of every thread,
-            // thread-minor, so each access instruction covers 4 KiB contiguously.
+            // thread-minor, so each access instruction covers 1 KiB contiguously.
+            constexpr uint32_t kChunkStride = kThreads * 16;
             auto store_own = [&]() {
                 const uint32_t base = lane_base(unit);
 #pragma unroll
@@ -379,7 +388,7 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
                             __builtin_amdgcn_raw_buffer_store_b128(
                                 f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                                       acc[i][j][4 * q + 3]},
-                                rs_part, base + ((i * SN + j) * 4 + q) * 4096, 0, kSc1);
+                                rs_part, base + ((i * SN + j) * 4 + q) * kChunkStride, 0, kSc1);
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             };
             if (tid == 0)
@@ -411,7 +420,7 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
 #pragma unroll
                     for (int c = 0; c < SN * 4; ++c)
                         dst[c] = __builtin_amdgcn_raw_buffer_load_b128(
-                            rs_part, base + (i * SN * 4 + c) * 4096, 0, kSc1);
+                            rs_part, base + (i * SN * 4 + c) * kChunkStride, 0, kSc1);
                 };
                 load_block(0, x[0]);
 #pragma unroll
@@ -482,7 +491,7 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
 
         // Coalesced store of the tile: 16-byte chunks, consecutive threads along a row.
         constexpr int kChunksPerRow = BN / 8;
-        for (int idx = tid; idx < BM * kChunksPerRow; idx += 256) {
+        for (int idx = tid; idx < BM * kChunksPerRow; idx += kThreads) {
             const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
             const int gr = row0 + row, gc = col0 + 8 * c;
             if constexpr (S == Stage::Apply) {
@@ -512,7 +521,7 @@ __global__ __launch_bounds__(256) void polar_stream_kernel(GemmArgs g) {
         if constexpr (S != Stage::Apply) {
             if (!diag) {
                 constexpr int kMirrorChunks = BM / 8;  // 16-byte chunks per mirror row
-                for (int idx = tid; idx < BN * kMirrorChunks; idx += 256) {
+                for (int idx = tid; idx < BN * kMirrorChunks; idx += kThreads) {
                     const int mc = idx / kMirrorChunks, rb = idx % kMirrorChunks;
                     uint32_t hh[8];
 #pragma unroll
@@ -531,75 +540,93 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *p, int64_t n)
 }
 
 template <int BM, int BN, Stage S>
-hipError_t launch_stream_one(const GemmArgs &g, int grid, hipStream_t stream) {
+hipError_t launch_stream_one(const GemmArgs &g, int grid, int waves, hipStream_t stream) {
     GemmArgs copy = g;
     void *args[] = {&copy};
-    return hipLaunchKernel(reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S>),
+    if constexpr (BM == 256 && BN == 256) {
+        if (waves == 8)
+            return hipLaunchKernel(reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, 8>),
+                                   dim3(grid), dim3(512), args, 0, stream);
+    }
+    if (waves != 4) return hipErrorInvalidValue;
+    return hipLaunchKernel(reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, 4>),
                            dim3(grid), dim3(256), args, 0, stream);
 }
 
 template <Stage S>
-hipError_t launch_stream_by_tile(int bm, int bn, const GemmArgs &g, int grid, hipStream_t stream) {
-    if (bm == 64 && bn == 64) return launch_stream_one<64, 64, S>(g, grid, stream);
-    if (bm == 128 && bn == 128) return launch_stream_one<128, 128, S>(g, grid, stream);
-    if (bm == 256 && bn == 256) return launch_stream_one<256, 256, S>(g, grid, stream);
+hipError_t launch_stream_by_tile(int bm, int bn, int waves, const GemmArgs &g, int grid,
+                                 hipStream_t stream) {
+    if (bm == 64 && bn == 64) return launch_stream_one<64, 64, S>(g, grid, waves, stream);
+    if (bm == 128 && bn == 128) return launch_stream_one<128, 128, S>(g, grid, waves, stream);
+    if (bm == 256 && bn == 256) return launch_stream_one<256, 256, S>(g, grid, waves, stream);
     if constexpr (S != Stage::Apply) {
-        if (bm == 192 && bn == 192) return launch_stream_one<192, 192, S>(g, grid, stream);
+        if (bm == 192 && bn == 192) return launch_stream_one<192, 192, S>(g, grid, waves, stream);
     }
     if constexpr (S == Stage::Apply) {
-        if (bm == 128 && bn == 256) return launch_stream_one<128, 256, S>(g, grid, stream);
-        if (bm == 256 && bn == 128) return launch_stream_one<256, 128, S>(g, grid, stream);
+        if (bm == 128 && bn == 256) return launch_stream_one<128, 256, S>(g, grid, waves, stream);
+        if (bm == 256 && bn == 128) return launch_stream_one<256, 128, S>(g, grid, waves, stream);
     }
     return hipErrorInvalidValue;
 }
 
 template <int BM, int BN, Stage S>
-int occupancy_one() {
+int occupancy_one(int waves) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S>), 256, 0) != hipSuccess)
-        return 0;
-    return n;
+    hipError_t e = hipErrorInvalidValue;
+    if constexpr (BM == 256 && BN == 256) {
+        if (waves == 8)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &n, reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, 8>), 512, 0);
+    }
+    if (waves == 4)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, 4>), 256, 0);
+    return e == hipSuccess ? n : 0;
 }
 
 template <Stage S>
-int occupancy_by_tile(int bm, int bn) {
-    if (bm == 64 && bn == 64) return occupancy_one<64, 64, S>();
-    if (bm == 128 && bn == 128) return occupancy_one<128, 128, S>();
-    if (bm == 256 && bn == 256) return occupancy_one<256, 256, S>();
+int occupancy_by_tile(int bm, int bn, int waves) {
+    if (bm == 64 && bn == 64) return occupancy_one<64, 64, S>(waves);
+    if (bm == 128 && bn == 128) return occupancy_one<128, 128, S>(waves);
+    if (bm == 256 && bn == 256) return occupancy_one<256, 256, S>(waves);
     if constexpr (S != Stage::Apply) {
-        if (bm == 192 && bn == 192) return occupancy_one<192, 192, S>();
+        if (bm == 192 && bn == 192) return occupancy_one<192, 192, S>(waves);
     }
     if constexpr (S == Stage::Apply) {
-        if (bm == 128 && bn == 256) return occupancy_one<128, 256, S>();
-        if (bm == 256 && bn == 128) return occupancy_one<256, 128, S>();
+        if (bm == 128 && bn == 256) return occupancy_one<128, 256, S>(waves);
+        if (bm == 256 && bn == 128) return occupancy_one<256, 128, S>(waves);
     }
     return 0;
 }
 
 }  // namespace
 
-hipError_t launch_stream(Stage s, int bm, int bn, const GemmArgs &g, hipStream_t stream) {
+int stream_waves(int bm, int bn, int requested) {
+    return (bm == 256 && bn == 256 && requested == 8) ? 8 : 4;
+}
+
+hipError_t launch_stream(Stage s, int bm, int bn, int waves, const GemmArgs &g,
+                         hipStream_t stream) {
     const int grid = g.sk_units + 8 * g.per_xcd;
     switch (s) {
         case Stage::Gram:
-            return launch_stream_by_tile<Stage::Gram>(bm, bn, g, grid, stream);
+            return launch_stream_by_tile<Stage::Gram>(bm, bn, waves, g, grid, stream);
         case Stage::Poly:
-            return launch_stream_by_tile<Stage::Poly>(bm, bn, g, grid, stream);
+            return launch_stream_by_tile<Stage::Poly>(bm, bn, waves, g, grid, stream);
         case Stage::Apply:
-            return launch_stream_by_tile<Stage::Apply>(bm, bn, g, grid, stream);
+            return launch_stream_by_tile<Stage::Apply>(bm, bn, waves, g, grid, stream);
     }
     return hipErrorInvalidValue;
 }
 
-int stream_blocks_per_cu(Stage s, int bm, int bn) {
+int stream_blocks_per_cu(Stage s, int bm, int bn, int waves) {
     switch (s) {
         case Stage::Gram:
-            return occupancy_by_tile<Stage::Gram>(bm, bn);
+            return occupancy_by_tile<Stage::Gram>(bm, bn, waves);
         case Stage::Poly:
-            return occupancy_by_tile<Stage::Poly>(bm, bn);
+            return occupancy_by_tile<Stage::Poly>(bm, bn, waves);
         case Stage::Apply:
-            return occupancy_by_tile<Stage::Apply>(bm, bn);
+            return occupancy_by_tile<Stage::Apply>(bm, bn, waves);
     }
     return 0;
 }

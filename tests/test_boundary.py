@@ -183,7 +183,8 @@ def test_entry_points_validate_before_launch():
 
 @pytest.mark.parametrize("var,value", [("MUON_POLAR_GRAM_TILE", "96"), ("MUON_POLAR_POLY_TILE", "512"),
                                        ("MUON_POLAR_APPLY_TILE_M", "32"),
-                                       ("MUON_POLAR_APPLY_TILE_N", "100")])
+                                       ("MUON_POLAR_APPLY_TILE_N", "100"),
+                                       ("MUON_POLAR_WAVES", "6"), ("MUON_POLAR_STREAM_K", "2")])
 def test_bad_tuning_variable_is_a_config_error(monkeypatch, var, value):
     monkeypatch.setenv(var, value)
     with pytest.raises(capi.CapiError) as err:

@@ -339,6 +339,7 @@ def test_noncontiguous_input():
      "MUON_POLAR_APPLY_TILE_N": "128"},
     {"MUON_POLAR_APPLY_TILE_M": "128", "MUON_POLAR_APPLY_TILE_N": "256"},
     {"MUON_POLAR_GRAM_TILE": "192", "MUON_POLAR_POLY_TILE": "192"},
+    {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_APPLY_TILE_M": "256", "MUON_POLAR_WAVES": "8"},
     {"MUON_POLAR_GRAM_TILE": "192", "MUON_POLAR_POLY_TILE": "256"},
     {"MUON_POLAR_GRAM_TILE": "128", "MUON_POLAR_POLY_TILE": "192", "MUON_POLAR_APPLY_TILE_M": "256",
      "MUON_POLAR_APPLY_TILE_N": "128"},

@@ -75,7 +75,8 @@ def test_split_is_in_use(shape):
 
 @pytest.mark.parametrize("split", ["1", "0"])
 @pytest.mark.parametrize("shape,env", [(s, {}) for s in SPLIT_SHAPES] +
-                         [((1, 4096, 14336), BIG_TILES), ((2, 2048, 4096), BIG_TILES)])
+                         [((1, 4096, 14336), BIG_TILES), ((2, 2048, 4096), BIG_TILES),
+                          ((1, 4096, 14336), {**BIG_TILES, "MUON_POLAR_WAVES": "8"})])
 def test_exact_sums_are_bitwise(monkeypatch, shape, env, split):
     monkeypatch.setenv("MUON_POLAR_STREAM_K", split)
     for k, v in env.items():
