@@ -164,6 +164,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="only the headline step loop and three 1 GiB device copies (the "
+                         "calibration kernel of known size), for rocprofv3 runs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -182,6 +185,16 @@ def main() -> int:
     # ---- headline: [4096,14336], one step
     batch, m, n = HEADLINE
     x = make_input((m, n), seed=0).cuda()
+    if args.profile:
+        sec = time_calls(lambda: mf.polar_step(x, a, b, c), args.steps, args.warmup)
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)  # reads and writes exactly 1 GiB
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": "polar_step [4096,14336]", "steps": args.steps,
+                          "us_per_step": round(sec * 1e6, 2), "copy_bytes": 1 << 30}), flush=True)
+        return 0
     sec = time_calls(lambda: mf.polar_step(x, a, b, c), args.steps, args.warmup)
     flops = credited_flops(batch, m, n)
     tflops = flops / sec / 1e12
