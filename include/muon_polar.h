@@ -62,6 +62,8 @@ typedef struct muon_polar_shape_info {
     int64_t padded_rows;    /* extent and leading dimension of A and P (>= m) */
     size_t gram_bytes;      /* bytes of one [batch, padded_rows, padded_rows] bf16 buffer */
     size_t workspace_bytes; /* bytes for A and P (each 256-byte aligned) and the stream-K area */
+    size_t express_workspace_bytes; /* muon_polar_express: the above, one [batch, m, n] bf16
+                                       buffer and the normalisation partial sums */
 } muon_polar_shape_info;
 
 int muon_polar_query(int64_t batch, int64_t m, int64_t n, muon_polar_shape_info *info);
@@ -101,6 +103,18 @@ int muon_polar_poly(const void *gram, void *poly, void *workspace, size_t worksp
 int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
                      size_t workspace_bytes, int64_t batch, int64_t m, int64_t n, double a,
                      hipStream_t stream);
+
+/* Several steps in one call, optionally after the per-matrix normalisation
+ * X / (‖X‖_F·1.01 + 1e-6) with the rounding points of the reference recipe
+ * (bf16 norm, bf16 product and sum, fp32 division rounded to bf16).
+ * coefficients: `steps` triples (a, b, c), step i uses coefficients[3i..3i+2].
+ * `workspace` must hold info.express_workspace_bytes; x and y must not overlap;
+ * steps >= 1, or steps == 0 with normalize (y = normalised x).
+ * No reference counterpart: replaces the caller-side loop of the reference's
+ * examples/five_steps.py:17-20 (normalise, then one polar_step per triple). */
+int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace_bytes,
+                       int64_t batch, int64_t m, int64_t n, const double *coefficients,
+                       int64_t steps, int normalize, hipStream_t stream);
 
 /* Detail of the last failure on the calling thread ("" if none).
  * Replaces CheckAcl / aclGetRecentErrMsg (csrc/muon_polar_step_binding.cpp:72-75). */

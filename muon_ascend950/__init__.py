@@ -4,6 +4,6 @@
 ``muon_fusion_ascend950_amd``.
 """
 
-from muon_fusion_ascend950_amd import __version__, polar_step
+from muon_fusion_ascend950_amd import COEFFICIENTS, __version__, polar_express, polar_step
 
-__all__ = ["polar_step"]
+__all__ = ["polar_step", "polar_express", "COEFFICIENTS"]

@@ -2,13 +2,15 @@
 
 Drop-in for the reference package surface (``muon_ascend950/__init__.py:1-10``):
 importing loads the native library and registers ``muon_ascend950::polar_step``.
+``polar_express`` (normalise + several steps in one call) has no reference
+counterpart; it replaces the loop of the reference's ``examples/five_steps.py``.
 """
 
 from ._loader import load_library
 
 load_library()
 
-from .ops import polar_step  # noqa: E402
+from .ops import COEFFICIENTS, polar_express, polar_step  # noqa: E402
 
-__all__ = ["polar_step"]
+__all__ = ["COEFFICIENTS", "polar_express", "polar_step"]
 __version__ = "0.1.1"

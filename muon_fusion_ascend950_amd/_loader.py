@@ -57,9 +57,14 @@ def load_library() -> None:
     def fake_polar_step(x, a: float, b: float, c: float):
         return torch.empty_like(x, memory_format=torch.contiguous_format)
 
-    try:
-        torch.library.register_fake("muon_ascend950::polar_step")(fake_polar_step)
-    except RuntimeError as exc:
-        if "already has" not in str(exc):
-            raise
+    def fake_polar_express(x, coefficients, normalize: bool):
+        return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+    for name, fake in (("muon_ascend950::polar_step", fake_polar_step),
+                       ("muon_ascend950::polar_express", fake_polar_express)):
+        try:
+            torch.library.register_fake(name)(fake)
+        except RuntimeError as exc:
+            if "already has" not in str(exc):
+                raise
     _LOADED = True

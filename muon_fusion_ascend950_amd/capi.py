@@ -18,6 +18,7 @@ EXPORTED_FUNCTIONS = (
     "muon_polar_gram",
     "muon_polar_poly",
     "muon_polar_apply",
+    "muon_polar_express",
     "muon_polar_last_error",
     "muon_polar_version",
 )
@@ -34,6 +35,7 @@ class ShapeInfo(ctypes.Structure):
         ("padded_rows", ctypes.c_int64),
         ("gram_bytes", ctypes.c_size_t),
         ("workspace_bytes", ctypes.c_size_t),
+        ("express_workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -71,8 +73,10 @@ def load() -> ctypes.CDLL:
     lib.muon_polar_gram.argtypes = [vp, vp, vp, sz, i64, i64, i64, vp]
     lib.muon_polar_poly.argtypes = [vp, vp, vp, sz, i64, i64, i64, dbl, dbl, vp]
     lib.muon_polar_apply.argtypes = [vp, vp, vp, vp, sz, i64, i64, i64, dbl, vp]
+    lib.muon_polar_express.argtypes = [vp, vp, vp, sz, i64, i64, i64,
+                                       ctypes.POINTER(ctypes.c_double), i64, ctypes.c_int, vp]
     for name in ("muon_polar_query", "muon_polar_step", "muon_polar_gram", "muon_polar_poly",
-                 "muon_polar_apply"):
+                 "muon_polar_apply", "muon_polar_express"):
         getattr(lib, name).restype = ctypes.c_int
     lib.muon_polar_last_error.argtypes = []
     lib.muon_polar_last_error.restype = ctypes.c_char_p
@@ -131,6 +135,23 @@ def _ws(workspace):
     if workspace is None:
         return None, 0
     return workspace.data_ptr(), workspace.numel() * workspace.element_size()
+
+
+def alloc_express_workspace(batch: int, m: int, n: int, device="cuda"):
+    import torch
+
+    info = query(batch, m, n)
+    return torch.empty(info.express_workspace_bytes, dtype=torch.uint8, device=device), info
+
+
+def express(x, y, workspace, coefficients, normalize: bool = True, stream=None) -> None:
+    """muon_polar_express: coefficients is a sequence of (a, b, c) triples."""
+    batch, m, n = _bmn(x)
+    flat = [float(v) for triple in coefficients for v in triple]
+    arr = (ctypes.c_double * max(1, len(flat)))(*flat)
+    check("muon_polar_express", load().muon_polar_express(
+        x.data_ptr(), y.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        batch, m, n, arr, len(flat) // 3, int(bool(normalize)), _stream(stream)))
 
 
 def gram(x, gram_buf, stream=None, workspace=None) -> None:

@@ -117,6 +117,9 @@ struct Plan {
     bool sk_any;
     int64_t counter_stride;
     size_t counters_offset, partials_offset;
+    // muon_polar_express: one [batch, m, n] bf16 buffer, then the normalisation
+    // partial sums, after the step's workspace
+    size_t express_x_offset, express_norm_offset, express_workspace_bytes;
 };
 
 std::mutex g_plan_mutex;
@@ -283,6 +286,11 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.partials_offset =
         p.counters_offset + align256(size_t(3) * p.counter_stride * sizeof(uint32_t));
     p.workspace_bytes = p.partials_offset + align256(partial_bytes);
+    p.express_x_offset = p.workspace_bytes;
+    p.express_norm_offset = p.express_x_offset + align256(size_t(batch) * m * n * 2u);
+    p.express_workspace_bytes =
+        p.express_norm_offset +
+        align256(size_t(batch) * muon_polar::norm_chunks(m * n) * sizeof(float));
     g_plans.emplace(key, p);
     out = p;
     return MUON_POLAR_OK;
@@ -454,6 +462,7 @@ int muon_polar_query(int64_t batch, int64_t m, int64_t n, muon_polar_shape_info 
     info->padded_rows = p.mp;
     info->gram_bytes = p.gram_bytes;
     info->workspace_bytes = p.workspace_bytes;
+    info->express_workspace_bytes = p.express_workspace_bytes;
     return MUON_POLAR_OK;
 }
 
@@ -532,6 +541,74 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
     st = run_poly(p, gram, poly, batch, b, c, &area_poly, stream);
     if (st != MUON_POLAR_OK) return st;
     return run_apply(p, poly, x, y, batch, m, n, a, &area_apply, stream);
+}
+
+int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace_bytes,
+                       int64_t batch, int64_t m, int64_t n, const double *coefficients,
+                       int64_t steps, int normalize, hipStream_t stream) {
+    if (x == nullptr || y == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    if (steps < 0 || (steps == 0 && !normalize))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "steps must be >= 1 (or 0 with normalize)");
+    if (steps > 0 && coefficients == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "coefficients is null");
+    Plan p{};
+    int st = get_plan(batch, m, n, p);
+    if (st != MUON_POLAR_OK) return st;
+    if (workspace == nullptr || workspace_bytes < p.express_workspace_bytes)
+        return fail(MUON_POLAR_ERR_WORKSPACE,
+                    "workspace must hold " + std::to_string(p.express_workspace_bytes) +
+                        " bytes, got " + std::to_string(workspace == nullptr ? 0 : workspace_bytes));
+    if (!aligned16(workspace))
+        return fail(MUON_POLAR_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+    const uintptr_t xb = reinterpret_cast<uintptr_t>(x), yb = reinterpret_cast<uintptr_t>(y);
+    const uintptr_t bytes = static_cast<uintptr_t>(batch * m * n * 2);
+    if (xb < yb + bytes && yb < xb + bytes)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "x and y must not overlap");
+
+    char *ws = static_cast<char *>(workspace);
+    void *gram = ws;
+    void *poly = ws + align256(p.gram_bytes);
+    uint16_t *scratch = reinterpret_cast<uint16_t *>(ws + p.express_x_offset);
+    float *partial = reinterpret_cast<float *>(ws + p.express_norm_offset);
+    uint16_t *out = static_cast<uint16_t *>(y);
+    // Buffer holding the iterate after step i (i = 0: the normalised input): the
+    // iterates alternate between y and the scratch buffer so that the last one is y.
+    auto iterate = [&](int64_t i) { return (steps - i) % 2 == 0 ? out : scratch; };
+
+    const uint16_t *cur = static_cast<const uint16_t *>(x);
+    if (normalize) {
+        uint16_t *dst = iterate(0);
+        const bool vec = (m * n) % 8 == 0 && aligned16(x) && aligned16(dst);
+        st = finish_stage(muon_polar::launch_normalize(cur, dst, partial, batch, m * n, vec, stream),
+                          stream, "normalize");
+        if (st != MUON_POLAR_OK) return st;
+        cur = dst;
+    }
+    if (steps > 0 && p.sk_any) {
+        // The stage kernels leave every counter they use at zero, so one clear
+        // covers all steps.
+        st = finish_stage(muon_polar::launch_zero_words(
+                              reinterpret_cast<uint32_t *>(ws + p.counters_offset),
+                              3 * p.counter_stride, stream),
+                          stream, "counter reset");
+        if (st != MUON_POLAR_OK) return st;
+    }
+    const SkArea area_gram = sk_area(p, workspace, 0), area_poly = sk_area(p, workspace, 1),
+                 area_apply = sk_area(p, workspace, 2);
+    for (int64_t i = 0; i < steps; ++i) {
+        const double a = coefficients[3 * i], b = coefficients[3 * i + 1],
+                     c = coefficients[3 * i + 2];
+        uint16_t *next = iterate(i + 1);
+        st = run_gram(p, cur, gram, batch, m, n, &area_gram, stream);
+        if (st != MUON_POLAR_OK) return st;
+        st = run_poly(p, gram, poly, batch, b, c, &area_poly, stream);
+        if (st != MUON_POLAR_OK) return st;
+        st = run_apply(p, poly, cur, next, batch, m, n, a, &area_apply, stream);
+        if (st != MUON_POLAR_OK) return st;
+        cur = next;
+    }
+    return MUON_POLAR_OK;
 }
 
 const char *muon_polar_last_error(void) { return g_last_error.c_str(); }

@@ -67,4 +67,12 @@ int stream_blocks_per_cu(Stage s, int bm, int bn, int waves);
 // Sets n 32-bit words at p to zero (stream-ordered, no memset node).
 hipError_t launch_zero_words(uint32_t *p, int64_t n, hipStream_t stream);
 
+// Per-matrix normalisation y = x / (‖x‖_F·1.01 + 1e-6) of `batch` matrices of mn
+// elements (reference recipe rounding points; polar_norm.hip).  `partial` holds
+// batch * norm_chunks(mn) floats; vec: mn % 8 == 0 and 16-byte aligned x and y.
+constexpr int64_t kNormChunk = 256 * 8 * 32;  // elements per partial sum
+int64_t norm_chunks(int64_t mn);
+hipError_t launch_normalize(const uint16_t *x, uint16_t *y, float *partial, int64_t batch,
+                            int64_t mn, bool vec, hipStream_t stream);
+
 }  // namespace muon_polar

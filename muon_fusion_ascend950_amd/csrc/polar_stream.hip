@@ -407,6 +407,9 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                 last = __builtin_amdgcn_readfirstlane(s_arrived) == others;
             }
             if (!last) continue;
+            // Every other contributor has counted itself in: the counter is this
+            // unit's alone now.  Leave it at zero for the next launch that uses it.
+            if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             // Own partial first or second in the order: add the others to it in
             // place (x + y == y + x).  Further back: start from p(u1) in memory.
             const bool from_memory = u1 - unit >= 2;

@@ -27,6 +27,8 @@ What it restates (reference file:line):
 * ``pad_crop_step`` — the reference binding's pad-to-128/16 + crop semantics
   (``csrc/muon_polar_step_binding.cpp:630-672``), to show masking equals padding.
 * ``wrapper_step`` — the Python wrapper's M > N transpose policy (``muon_ascend950/ops.py:24-33``).
+* ``normalize_reference_rounding`` — the normalisation of ``tests/test_polar_step.py:39`` and
+  ``examples/five_steps.py:18`` with torch's bf16 rounding points (for ``polar_express``).
 * ``sparse_sign_input`` / ``polar_step_fused_sparse`` — ``polar_step_fused`` on sparse ±1
   inputs whose sums are exact in fp32 in any order, so a kernel must match it bit for bit
   at full size whatever its K split (no reference counterpart: a test device).
@@ -97,6 +99,21 @@ def make_input(shape, seed: int = 0):
     gen = torch.Generator().manual_seed(seed)
     x = torch.randn(shape, dtype=torch.bfloat16, generator=gen)
     return x / (x.norm(dim=(-2, -1), keepdim=True) * 1.01 + 1e-6)
+
+
+def normalize_reference_rounding(x: np.ndarray) -> np.ndarray:
+    """x / (‖x‖_F·1.01 + 1e-6) per matrix with the rounding points of the reference
+    recipe as torch evaluates it on bf16 tensors (tests/test_polar_step.py:39,
+    examples/five_steps.py:18): the norm rounded to bf16, the product with 1.01 (as
+    fp32) rounded to bf16, the sum with 1e-6 (as fp32) rounded to bf16, then an fp32
+    division rounded to bf16.  The sum of squares is exact (float64) here; a kernel
+    summing in fp32 can differ only where the norm sits at a bf16 rounding boundary.
+    x must hold bf16 values (float64 array)."""
+    x = np.asarray(x, dtype=np.float64)
+    norm = bf16_round(np.sqrt((x * x).sum(axis=(-2, -1), keepdims=True)))
+    d = bf16_round(norm * np.float32(1.01))
+    d = bf16_round(d + np.float32(1e-6))
+    return bf16_round(x.astype(np.float32) / d).astype(np.float64)
 
 
 def to_numpy_f64(t) -> np.ndarray:

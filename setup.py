@@ -9,9 +9,16 @@ from setuptools.command.build_ext import build_ext
 
 class InPlaceHipBuild(build_ext):
     def run(self):
-        from muon_fusion_ascend950_amd import _build
+        # Load the build script by path: importing the package would load the native
+        # library that is being built (missing or stale at this point).
+        import importlib.util
+        from pathlib import Path
 
-        _build.build(verbose=True)
+        path = Path(__file__).resolve().parent / "muon_fusion_ascend950_amd" / "_build.py"
+        spec = importlib.util.spec_from_file_location("muon_fusion_ascend950_amd_build", path)
+        module = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(module)
+        module.build(verbose=True)
 
 
 setup(

@@ -20,6 +20,7 @@ import torch
 from torch._subclasses.fake_tensor import FakeTensorMode
 
 import muon_fusion_ascend950_amd as mf
+from oracle import polar_oracle as O
 from muon_fusion_ascend950_amd import _loader, capi
 
 ROOT = Path(__file__).resolve().parent.parent
@@ -32,8 +33,11 @@ def test_public_surface():
     import muon_ascend950
 
     assert muon_ascend950.polar_step is mf.polar_step
+    assert muon_ascend950.polar_express is mf.polar_express
     assert mf.__version__ == "0.1.1" == muon_ascend950.__version__
-    assert mf.__all__ == ["polar_step"]
+    assert mf.__all__ == ["COEFFICIENTS", "polar_express", "polar_step"]
+    # the reference's five triples (tests/test_polar_step.py:13-19)
+    assert mf.COEFFICIENTS == tuple(tuple(t) for t in O.COEFFICIENTS)
 
 
 def test_rejects_non_tensor():
@@ -84,6 +88,43 @@ def test_fake_kernel_on_op_directly():
 def test_op_schema_matches_reference():
     schema = str(torch.ops.muon_ascend950.polar_step.default._schema)
     assert schema == "muon_ascend950::polar_step(Tensor x, float a, float b, float c) -> Tensor"
+
+
+def test_express_fake_and_schema():
+    schema = str(torch.ops.muon_ascend950.polar_express.default._schema)
+    assert schema == ("muon_ascend950::polar_express(Tensor x, float[] coefficients, bool normalize)"
+                      " -> Tensor")
+    with FakeTensorMode():
+        for shape in [(2, 5, 9), (9, 5), (3, 40, 7)]:
+            x = torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+            y = mf.polar_express(x)
+            assert y.shape == x.shape and y.dtype == torch.bfloat16
+
+
+def test_express_rejects_bad_arguments():
+    with FakeTensorMode():
+        x = torch.empty(2, 5, 9, dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(ValueError, match="triples"):
+            mf.polar_express(x, [(1.0, 2.0)])
+        with pytest.raises(ValueError, match="nothing to do"):
+            mf.polar_express(x, [], normalize=False)
+        with pytest.raises(TypeError, match="bfloat16"):
+            mf.polar_express(x.float())
+
+
+def test_express_entry_validates_before_launch():
+    lib = capi.load()
+    coeffs = (ctypes.c_double * 3)(1.0, 2.0, 3.0)
+    info = capi.query(1, 4, 8)
+    assert info.express_workspace_bytes >= info.workspace_bytes + 4 * 8 * 2
+    big = info.express_workspace_bytes
+    assert lib.muon_polar_express(None, 16, 16, big, 1, 4, 8, coeffs, 1, 1, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_express(16, 4096, 16, big, 1, 4, 8, coeffs, 0, 0, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_express(16, 4096, 16, big, 1, 4, 8, None, 2, 1, None) == capi.ERR_INVALID_ARGUMENT
+    assert lib.muon_polar_express(16, 4096, 16, big - 1, 1, 4, 8, coeffs, 1, 1, None) == capi.ERR_WORKSPACE
+    # x and y overlap: rejected before anything launches (pointers never dereferenced)
+    assert lib.muon_polar_express(16, 32, 16, big, 1, 4, 8, coeffs, 1, 1, None) == capi.ERR_INVALID_ARGUMENT
+    assert "overlap" in capi.last_error()
 
 
 def test_loader_is_idempotent():
@@ -203,3 +244,17 @@ def test_tuning_variables_enter_the_plan(monkeypatch):
     assert capi.query(1, 300, 700).padded_rows == 384
     monkeypatch.setenv("MUON_POLAR_POLY_TILE", "256")
     assert capi.query(1, 300, 700).padded_rows == 768
+
+
+def test_build_entry_does_not_import_the_package():
+    """build() must work before a native library exists (or when the one in place is
+    stale): it loads the build script by path, never the package."""
+    import subprocess
+    import sys
+
+    code = ("import sys, __graft_entry__ as g; m = g._load_builder(); "
+            "assert callable(m.build); "
+            "assert 'muon_fusion_ascend950_amd' not in sys.modules, 'package imported'")
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

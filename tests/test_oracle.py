@@ -285,3 +285,35 @@ def test_exact_sums_catch_a_dropped_or_doubled_k_range():
         gram = O.bf16_round(doubled).astype(np.float64)
         poly = O.bf16_round(-gram + gram @ gram).astype(np.float64)
         assert not np.array_equal(O.bf16_round(2.0 * d + poly @ d), y_ok)
+
+
+# ----------------------------------------------------------------------------- normalisation
+@pytest.mark.parametrize("shape", [(3, 40, 70), (1, 129, 130), (2, 8, 2048)])
+def test_normalization_matches_torch_bf16_recipe(shape):
+    """The restatement reproduces the reference recipe run by torch in bf16 (CPU)."""
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(shape, dtype=torch.bfloat16, generator=gen) * 3.0
+    want = x / (x.norm(dim=(-2, -1), keepdim=True) * 1.01 + 1e-6)
+    got = O.normalize_reference_rounding(O.to_numpy_f64(x))
+    wb = want.contiguous().view(torch.int16).numpy().view(np.uint16)
+    gb = O.f32_to_bf16_bits(got.astype(np.float32))
+    assert O.bf16_ulp_distance(gb, wb).max() <= 1
+    assert (gb != wb).mean() < 1e-3
+
+
+def test_normalization_closed_forms():
+    # a single nonzero v: norm = |v|, d = bf16(bf16(|v|·1.01) + 1e-6)
+    x = np.zeros((1, 3, 4))
+    x[0, 1, 2] = -2.5
+    got = O.normalize_reference_rounding(x)
+    d = O.bf16_round(O.bf16_round(np.float32(2.5) * np.float32(1.01)) + np.float32(1e-6)).item()
+    assert got[0, 1, 2] == O.bf16_round(np.float32(-2.5) / np.float32(d)).item()
+    assert np.count_nonzero(got) == 1
+    # zero matrix: d = bf16(1e-6) > 0, output exactly zero (no NaN)
+    z = O.normalize_reference_rounding(np.zeros((2, 4, 5)))
+    assert not np.isnan(z).any() and not z.any()
+    # planted mistake: dropping the 1.01 factor changes the result
+    x = O.to_numpy_f64(torch.randn(2, 16, 40, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16))
+    norm = O.bf16_round(np.sqrt((x * x).sum(axis=(-2, -1), keepdims=True)))
+    wrong = O.bf16_round(x.astype(np.float32) / O.bf16_round(norm + np.float32(1e-6)))
+    assert not np.array_equal(wrong, O.normalize_reference_rounding(x))
