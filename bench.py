@@ -212,6 +212,18 @@ def main() -> int:
     # bytes that must move at least: X in, Y out; with A and P stored: + 4·B·M²·2 + X re-read
     hbm2 = 2 * b2 * m2 * n2 * 2 + 4 * b2 * m2 * m2 * 2 + b2 * m2 * n2 * 2
 
+    # five steps after the normalisation (the reference's examples/five_steps.py loop):
+    # one polar_express call vs normalisation in torch + five polar_step calls
+    raw = make_input((m, n), seed=1) * 3.0
+    def reference_loop():
+        y = raw / (raw.norm(dim=(-2, -1), keepdim=True) * 1.01 + 1e-6)
+        for a_, b_, c_ in mf.COEFFICIENTS:
+            y = mf.polar_step(y, a_, b_, c_)
+        return y
+    raw = raw.cuda()
+    sec_express = time_calls(lambda: mf.polar_express(raw), 10, 3)
+    sec_loop = time_calls(reference_loop, 10, 3)
+
     # PyTorch eager on the same GPU (the reference's comparison point, README.md:172-208)
     eager = time_calls(lambda: torch_eager(x), 10, 3)
     eager2 = time_calls(lambda: torch_eager(x2), 50, 5)
@@ -249,6 +261,12 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": traffic,
+        },
+        "five_step": {
+            "workload": "normalise + 5 steps on bf16 [4096,14336] (examples/five_steps.py loop)",
+            "polar_express_us": round(sec_express * 1e6, 2),
+            "torch_norm_plus_5_polar_step_us": round(sec_loop * 1e6, 2),
+            "tflops": round(5 * flops / sec_express / 1e12, 2),
         },
         "secondary": {
             "workload": "polar_step on bf16 [8,512,2048], one step",
