@@ -128,14 +128,19 @@ std::unordered_map<PlanKey, Plan, PlanKeyHash> g_plans;
 // Default tile shapes by matrix size (measured on MI355X).  256x256 tiles run
 // with 8 waves (two per SIMD: one wave's LDS and barrier waits are covered by
 // the other's MFMAs), 12% faster per step than 4 waves at 4096 x 14336.  The
-// triangular stages use them from m = 4096; below that, 128x128 tiles (two
-// workgroups per CU) are faster there (2x at m = 2048, where a 256x256 grid
-// has too few tiles).  Stage 3 has 4x more tiles and prefers 256x256 from
-// m = 1024.  Small matrices use 64x64 tiles to put enough workgroups on the
-// 256 CUs.
+// gram stage uses them from m = 3072 (its K = n is long), the poly stage from
+// m = 4096; below that, 128x128 tiles (two workgroups per CU) are faster (2x
+// at m = 2048, where a 256x256 grid has too few tiles; poly at m = 3072: 54 vs
+// 82 us).  Stage 3 has 4x more tiles and prefers 256x256 from m = 1024.  Small
+// matrices use 64x64 tiles to put enough workgroups on the 256 CUs.
 constexpr uint32_t kDefaultWaves = 8;
 
-uint32_t default_square_tile(int64_t m) {
+uint32_t default_gram_tile(int64_t m) {
+    if (m >= 3072) return 256;
+    if (m > 256) return 128;
+    return 64;
+}
+uint32_t default_poly_tile(int64_t m) {
     if (m >= 4096) return 256;
     if (m > 256) return 128;
     return 64;
@@ -148,9 +153,11 @@ uint32_t default_apply_tile(int64_t m) {
 
 int read_knobs(int64_t m, int64_t n, Knobs &k) {
     (void)n;
-    const uint32_t def = default_square_tile(m);
-    k.gram_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_TILE", def));
-    k.poly_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_POLY_TILE", k.gram_tile));
+    k.gram_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_TILE", default_gram_tile(m)));
+    // an explicit gram tile also sets the poly tile unless that is given too
+    const bool gram_set = std::getenv("MUON_POLAR_GRAM_TILE") != nullptr;
+    k.poly_tile = static_cast<uint32_t>(
+        env_u64("MUON_POLAR_POLY_TILE", gram_set ? k.gram_tile : default_poly_tile(m)));
     k.apply_bm = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_M", default_apply_tile(m)));
     k.apply_bn = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_N", k.apply_bm));
     k.stream = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM", 1));
@@ -442,7 +449,11 @@ int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t b
     g.s_acc = 1.0f;
     g.bytes_row = static_cast<uint32_t>(p.mp * p.mp * 2);
     g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
-    g.group_n = static_cast<int32_t>(std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", 8)));
+    // Column tiles per raster group: 8 for wide X (4096 x 14336: 56 column tiles),
+    // 4 for narrower ones (n = 4096: 16 column tiles; 476 vs 498 us).
+    const uint64_t group_default = p.apply_tn >= 32 ? 8 : 4;
+    g.group_n = static_cast<int32_t>(
+        std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", group_default)));
     const bool vec = (n % 8 == 0) && aligned16(x) && aligned16(y);
     return finish_stage(launch_stage(Stage::Apply, p.apply_bm, p.apply_bn, p.waves[2],
                                      p.stream && vec, vec,
