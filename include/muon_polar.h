@@ -7,12 +7,18 @@
  *     P = b·A + c·A·A   (stage 2, "poly":  A·A with the polynomial in the epilogue)
  *     Y = a·X + P·X     (stage 3, "apply": P·X with the a·X add in the epilogue)
  *
- * X and Y are row-major contiguous bf16 tensors of shape [batch, m, n] with
- * 1 <= m <= n.  A and P live in a caller-provided scratch ("workspace") of
- * shape [batch, padded_rows, padded_rows] each, where padded_rows >= m is the
- * stage tile multiple reported by muon_polar_query().  The padding rows and
- * columns of A and P are written as exact zeros by the kernels, so no caller
- * memset is needed.
+ * X and Y are row-major contiguous bf16 tensors of shape [batch, m, n].  For
+ * m > n, muon_polar_step and muon_polar_express run the right-Gram form
+ *
+ *     G = Xᵀ·X,   P = b·G + c·G²,   Y = a·X + X·P
+ *
+ * (the step of the transposed input, transposed back, without the copies; it
+ * needs n % 8 == 0 and 16-byte aligned x and y, and A below is then G).  A and
+ * P live in a caller-provided scratch ("workspace") of shape [batch,
+ * padded_rows, padded_rows] each, where padded_rows >= min(m, n) is the stage
+ * tile multiple reported by muon_polar_query().  The padding rows and columns
+ * of A and P are written as exact zeros by the kernels, so no caller memset is
+ * needed.
  *
  * Stream-K: when the last round of a stage's output tiles would leave most CUs
  * idle, the K loops of those tiles are cut into equal shares, one per
@@ -69,9 +75,12 @@ typedef struct muon_polar_shape_info {
 int muon_polar_query(int64_t batch, int64_t m, int64_t n, muon_polar_shape_info *info);
 
 /* Whole step: Y = a·X + (b·A + c·A²)·X with A = X·Xᵀ, three kernels in order
- * on `stream`.  `workspace` must hold info.workspace_bytes.
+ * on `stream` (m > n: the right-Gram form above).  `workspace` must hold
+ * info.workspace_bytes.
  * Replaces MuonPolarStepAscend950 (csrc/muon_polar_step_binding.cpp:613-673)
- * without its pad/crop copies: edges are masked in the kernels. */
+ * without its pad/crop copies: edges are masked in the kernels.  The reference
+ * rejects m > n there (binding.cpp:622-624) and transposes in its Python
+ * wrapper (muon_ascend950/ops.py:26-32). */
 int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_bytes,
                     int64_t batch, int64_t m, int64_t n,
                     double a, double b, double c, hipStream_t stream);
@@ -81,7 +90,7 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
  * info.workspace_bytes, the same one muon_polar_step takes (gram / poly may be
  * its A / P areas), which lets the stage use the stream-K split exactly as
  * inside muon_polar_step.  The reference's stage launchers likewise take a
- * device-side buffer (their tiling struct). */
+ * device-side buffer (their tiling struct).  The stages take m <= n only. */
 
 /* Stage 1: gram[bt] = X[bt]·X[bt]ᵀ into a [batch, padded_rows, padded_rows]
  * bf16 buffer (padding written as zeros).
@@ -109,7 +118,8 @@ int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
  * (bf16 norm, bf16 product and sum, fp32 division rounded to bf16).
  * coefficients: `steps` triples (a, b, c), step i uses coefficients[3i..3i+2].
  * `workspace` must hold info.express_workspace_bytes; x and y must not overlap;
- * steps >= 1, or steps == 0 with normalize (y = normalised x).
+ * steps >= 1, or steps == 0 with normalize (y = normalised x); m > n as for
+ * muon_polar_step.
  * No reference counterpart: replaces the caller-side loop of the reference's
  * examples/five_steps.py:17-20 (normalise, then one polar_step per triple). */
 int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace_bytes,

@@ -61,6 +61,7 @@ def load_library() -> None:
         return torch.empty_like(x, memory_format=torch.contiguous_format)
 
     for name, fake in (("muon_ascend950::polar_step", fake_polar_step),
+                       ("muon_ascend950::polar_step_tall", fake_polar_step),
                        ("muon_ascend950::polar_express", fake_polar_express)):
         try:
             torch.library.register_fake(name)(fake)

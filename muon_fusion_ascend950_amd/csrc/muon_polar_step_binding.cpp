@@ -46,9 +46,47 @@ at::Tensor MuonPolarStepHip(const at::Tensor &x, double a, double b, double c) {
     return out;
 }
 
+// Contiguous copy of x whose data is 16-byte aligned (the DMA-fed kernels that
+// run m > n need it; a fresh allocation always is).
+at::Tensor aligned_contiguous(const at::Tensor &x) {
+    at::Tensor t = x.contiguous();
+    if (reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 != 0) t = t.clone();
+    return t;
+}
+
+// One step on X [batch, M, N] with M > N in the right-Gram form
+// Y = a·X + X·(b·G + c·G²), G = Xᵀ·X: no transposed copies of X and Y (the
+// reference's wrapper transposes around the op, ops.py:26-32).  Needs N % 8 == 0.
+at::Tensor MuonPolarStepTallHip(const at::Tensor &x, double a, double b, double c) {
+    TORCH_CHECK(x.defined(), "muon_polar_step_tall: x must be defined");
+    TORCH_CHECK(x.device().is_cuda(), "muon_polar_step_tall: x must be a ROCm (HIP) device tensor");
+    TORCH_CHECK(x.scalar_type() == at::kBFloat16, "muon_polar_step_tall: only bfloat16 is supported");
+    TORCH_CHECK(x.dim() == 3, "muon_polar_step_tall: x must have shape [batch, M, N]");
+    TORCH_CHECK(x.size(0) > 0 && x.size(1) > 0 && x.size(2) > 0,
+                "muon_polar_step_tall: all dimensions must be positive");
+    TORCH_CHECK(x.size(1) > x.size(2) && x.size(2) % 8 == 0,
+                "muon_polar_step_tall: expects M > N with N % 8 == 0");
+    const c10::OptionalDeviceGuard device_guard(x.device());
+    const at::Tensor input = aligned_contiguous(x);
+    const int64_t batch = input.size(0), m = input.size(1), n = input.size(2);
+    muon_polar_shape_info info{};
+    int st = muon_polar_query(batch, m, n, &info);
+    TORCH_CHECK(st == MUON_POLAR_OK, "muon_polar_step_tall: ", muon_polar_last_error());
+    at::Tensor workspace =
+        at::empty({static_cast<int64_t>(info.workspace_bytes)}, input.options().dtype(at::kByte));
+    at::Tensor out =
+        at::empty_like(input, input.options().memory_format(c10::MemoryFormat::Contiguous));
+    hipStream_t stream = c10::hip::getCurrentHIPStream(x.device().index()).stream();
+    st = muon_polar_step(input.data_ptr(), out.data_ptr(), workspace.data_ptr(),
+                         info.workspace_bytes, batch, m, n, a, b, c, stream);
+    TORCH_CHECK(st == MUON_POLAR_OK, "muon_polar_step_tall: ", muon_polar_last_error());
+    return out;
+}
+
 // Several steps (and the optional per-matrix normalisation) in one call; no
 // reference counterpart (the reference's examples/five_steps.py:17-20 loops in
-// Python).  Same preconditions as polar_step; coefficients are flattened triples.
+// Python).  Preconditions of polar_step, except that M > N is accepted when
+// N % 8 == 0 (right-Gram form); coefficients are flattened triples.
 at::Tensor MuonPolarExpressHip(const at::Tensor &x, at::ArrayRef<double> coefficients,
                                bool normalize) {
     TORCH_CHECK(x.defined(), "muon_polar_express: x must be defined");
@@ -57,14 +95,14 @@ at::Tensor MuonPolarExpressHip(const at::Tensor &x, at::ArrayRef<double> coeffic
     TORCH_CHECK(x.dim() == 3, "muon_polar_express: x must have shape [batch, M, N]");
     TORCH_CHECK(x.size(0) > 0 && x.size(1) > 0 && x.size(2) > 0,
                 "muon_polar_express: all dimensions must be positive");
-    TORCH_CHECK(x.size(1) <= x.size(2),
-                "muon_polar_express: expects M <= N; transpose policy stays outside this op");
+    TORCH_CHECK(x.size(1) <= x.size(2) || x.size(2) % 8 == 0,
+                "muon_polar_express: M > N needs N % 8 == 0; otherwise transpose outside this op");
     TORCH_CHECK(coefficients.size() % 3 == 0,
                 "muon_polar_express: coefficients must be (a, b, c) triples");
     TORCH_CHECK(!coefficients.empty() || normalize,
                 "muon_polar_express: no coefficients and no normalisation");
     const c10::OptionalDeviceGuard device_guard(x.device());
-    const at::Tensor input = x.contiguous();
+    const at::Tensor input = x.size(1) > x.size(2) ? aligned_contiguous(x) : x.contiguous();
     const int64_t batch = input.size(0), m = input.size(1), n = input.size(2);
 
     muon_polar_shape_info info{};
@@ -87,10 +125,12 @@ at::Tensor MuonPolarExpressHip(const at::Tensor &x, at::ArrayRef<double> coeffic
 
 TORCH_LIBRARY(muon_ascend950, m) {
     m.def("polar_step(Tensor x, float a, float b, float c) -> Tensor");
+    m.def("polar_step_tall(Tensor x, float a, float b, float c) -> Tensor");
     m.def("polar_express(Tensor x, float[] coefficients, bool normalize) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(muon_ascend950, CUDA, m) {
     m.impl("polar_step", &MuonPolarStepHip);
+    m.impl("polar_step_tall", &MuonPolarStepTallHip);
     m.impl("polar_express", &MuonPolarExpressHip);
 }

@@ -101,8 +101,10 @@ struct SkSplit {
 };
 
 struct Plan {
-    int64_t m;   // rows of X
-    int64_t mp;  // padded extent / leading dimension of A and P
+    int64_t m, n;  // X is [m, n]
+    int64_t s;     // min(m, n): extent of A and P (X·Xᵀ for m <= n, Xᵀ·X for m > n)
+    bool tall;     // m > n: the right-Gram stages (GramT, ApplyR)
+    int64_t mp;    // padded extent / leading dimension of A and P
     int gram_tile, poly_tile, apply_bm, apply_bn;
     int gram_nt, poly_nt;           // tiles per side of the triangular stages
     int apply_tm, apply_tn;         // tiles along rows / cols of stage 3
@@ -181,11 +183,9 @@ int read_knobs(int64_t m, int64_t n, Knobs &k) {
 int check_shape(int64_t batch, int64_t m, int64_t n) {
     if (batch <= 0 || m <= 0 || n <= 0)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "all dimensions must be positive");
-    if (m > n)
-        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
-                    "expects M <= N; the transpose policy stays outside this op");
     // 32-bit byte offsets inside one matrix (X and the padded A/P): < 2^31 bytes.
-    if (m * n >= (int64_t(1) << 30) || round_up(m, 256) * round_up(m, 256) >= (int64_t(1) << 30))
+    const int64_t s = std::min(m, n);
+    if (m * n >= (int64_t(1) << 30) || round_up(s, 256) * round_up(s, 256) >= (int64_t(1) << 30))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "matrix too large (2^30 elements or more)");
     if (batch > (int64_t(1) << 20))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "batch too large");
@@ -225,9 +225,13 @@ SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident
 int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     int st = check_shape(batch, m, n);
     if (st != MUON_POLAR_OK) return st;
+    const bool tall = m > n;
+    const int64_t small = std::min(m, n), large = std::max(m, n);
     Knobs knobs{};
-    st = read_knobs(m, n, knobs);
+    st = read_knobs(small, large, knobs);
     if (st != MUON_POLAR_OK) return st;
+    if (tall && knobs.gram_tile == 192)
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE=192 is not available for m > n");
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) device = -1;
     const PlanKey key{device, batch, m, n, knobs};
@@ -243,8 +247,11 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.apply_bm = static_cast<int>(knobs.apply_bm);
     p.apply_bn = static_cast<int>(knobs.apply_bn);
     p.m = m;
+    p.n = n;
+    p.s = small;
+    p.tall = tall;
     // A and P are tiled by both stage tiles: pad to a common multiple.
-    p.mp = round_up(m, std::lcm(p.gram_tile, p.poly_tile));
+    p.mp = round_up(small, std::lcm(p.gram_tile, p.poly_tile));
     if (p.mp * p.mp >= (int64_t(1) << 30))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "matrix too large (2^30 elements or more)");
     p.gram_nt = static_cast<int>(p.mp / p.gram_tile);
@@ -255,7 +262,9 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.poly_grid = batch * (int64_t(p.poly_nt) * (p.poly_nt + 1) / 2);
     p.apply_grid = batch * int64_t(p.apply_tm) * p.apply_tn;
     p.gram_bytes = static_cast<size_t>(batch) * p.mp * p.mp * 2u;
-    p.stream = knobs.stream != 0;
+    // The right-Gram stages exist only as DMA-fed kernels: MUON_POLAR_STREAM=0
+    // selects the register-staged kernels for m <= n alone.
+    p.stream = knobs.stream != 0 || tall;
     if (p.gram_grid >= (int64_t(1) << 31) || p.apply_grid >= (int64_t(1) << 31))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "grid too large");
 
@@ -268,9 +277,11 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
                        cus > 0;
     const int tiles_bm[3] = {p.gram_tile, p.poly_tile, p.apply_bm};
     const int tiles_bn[3] = {p.gram_tile, p.poly_tile, p.apply_bn};
-    const Stage stages[3] = {Stage::Gram, Stage::Poly, Stage::Apply};
+    const Stage stages[3] = {tall ? Stage::GramT : Stage::Gram, Stage::Poly,
+                             tall ? Stage::ApplyR : Stage::Apply};
     const int64_t grids[3] = {p.gram_grid, p.poly_grid, p.apply_grid};
-    const int64_t ksteps[3] = {round_up(n, 64) / 64, round_up(m, 64) / 64, round_up(m, 64) / 64};
+    const int64_t ksteps[3] = {round_up(large, 64) / 64, round_up(small, 64) / 64,
+                               round_up(small, 64) / 64};
     p.sk_any = false;
     p.counter_stride = 0;
     size_t partial_bytes = 0;
@@ -412,8 +423,8 @@ int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double 
     g.sb_row = g.sb_col = g.sb_epi = g.sb_out = p.mp * p.mp;
     g.ld_row = g.ld_col = g.ld_epi = g.ld_out = static_cast<int32_t>(p.mp);
     g.row_rows = g.col_rows = g.row_k = g.col_k = static_cast<int32_t>(p.mp);
-    // A is zero beyond row / column m: the K loop stops at m (rounded to a step).
-    g.k_loop = static_cast<int32_t>(round_up(p.m, 64));
+    // A is zero beyond row / column s: the K loop stops at s (rounded to a step).
+    g.k_loop = static_cast<int32_t>(round_up(p.s, 64));
     g.out_rows = g.out_cols = static_cast<int32_t>(p.mp);
     g.tiles_m = g.tiles_n = p.poly_nt;
     g.tiles_per_batch = p.poly_nt * (p.poly_nt + 1) / 2;
@@ -461,6 +472,92 @@ int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t b
                         stream, "apply");
 }
 
+// Right-Gram stages for m > n (X is [m, n]): G = Xᵀ·X over the n x n upper
+// tiles, both operands read N-contiguous from X's rows (K runs over the m rows).
+int run_gram_t(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
+               const SkArea *area, hipStream_t stream) {
+    GemmArgs g{};
+    g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(x);
+    g.out = static_cast<uint16_t *>(gram);
+    g.sb_row = g.sb_col = g.sb_epi = m * n;
+    g.sb_out = p.mp * p.mp;
+    g.ld_row = g.ld_col = g.ld_epi = static_cast<int32_t>(n);
+    g.ld_out = static_cast<int32_t>(p.mp);
+    g.row_rows = g.col_rows = static_cast<int32_t>(n);  // output index: columns of X
+    g.row_k = g.col_k = static_cast<int32_t>(m);        // contraction: rows of X
+    g.k_loop = static_cast<int32_t>(round_up(m, 64));
+    g.out_rows = g.out_cols = static_cast<int32_t>(p.mp);
+    g.tiles_m = g.tiles_n = p.gram_nt;
+    g.tiles_per_batch = p.gram_nt * (p.gram_nt + 1) / 2;
+    g.s_epi = 0.0f;
+    g.s_acc = 1.0f;
+    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
+    return finish_stage(launch_stage(Stage::GramT, p.gram_tile, p.gram_tile, p.waves[0], true, true,
+                                     g, batch, p.gram_grid, &p.sk[0], area, stream),
+                        stream, "gram");
+}
+
+// Y = a·X + X·P for m > n: X rows and P rows (P is symmetric) are both
+// K-contiguous; the output [m, n] and the a·X epilogue are stage 3's.
+int run_apply_r(const Plan &p, const void *poly, const void *x, void *y, int64_t batch,
+                int64_t m, int64_t n, double a, const SkArea *area, hipStream_t stream) {
+    GemmArgs g{};
+    g.rowop = g.epi = static_cast<const uint16_t *>(x);
+    g.colop = static_cast<const uint16_t *>(poly);
+    g.out = static_cast<uint16_t *>(y);
+    g.sb_row = g.sb_epi = g.sb_out = m * n;
+    g.sb_col = p.mp * p.mp;
+    g.ld_row = g.ld_epi = g.ld_out = static_cast<int32_t>(n);
+    g.ld_col = static_cast<int32_t>(p.mp);
+    g.row_rows = static_cast<int32_t>(m);
+    g.row_k = static_cast<int32_t>(n);
+    g.col_rows = g.col_k = static_cast<int32_t>(p.mp);
+    g.k_loop = static_cast<int32_t>(round_up(n, 64));  // P is zero beyond column n
+    g.out_rows = static_cast<int32_t>(m);
+    g.out_cols = static_cast<int32_t>(n);
+    g.tiles_m = p.apply_tm;
+    g.tiles_n = p.apply_tn;
+    g.tiles_per_batch = p.apply_tm * p.apply_tn;
+    g.s_epi = static_cast<float>(a);
+    g.s_acc = 1.0f;
+    g.bytes_row = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
+    g.bytes_col = static_cast<uint32_t>(p.mp * p.mp * 2);
+    const uint64_t group_default = p.apply_tn >= 32 ? 8 : 4;
+    g.group_n = static_cast<int32_t>(
+        std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", group_default)));
+    return finish_stage(launch_stage(Stage::ApplyR, p.apply_bm, p.apply_bn, p.waves[2], true, true,
+                                     g, batch, p.apply_grid, &p.sk[2], area, stream),
+                        stream, "apply");
+}
+
+// m > n runs only on the DMA-fed kernels.
+int check_tall(const Plan &p, const void *x, const void *y) {
+    if (p.n % 8 != 0 || !aligned16(x) || !aligned16(y))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
+                    "m > n runs the right-Gram form, which needs n % 8 == 0 and 16-byte aligned "
+                    "x and y; otherwise transpose outside");
+    return MUON_POLAR_OK;
+}
+
+// One step given the workspace areas: left form (m <= n) or right-Gram form.
+int run_step(const Plan &p, const void *x, void *y, void *gram, void *poly, const SkArea *areas,
+             int64_t batch, double a, double b, double c, hipStream_t stream) {
+    int st = p.tall ? run_gram_t(p, x, gram, batch, p.m, p.n, &areas[0], stream)
+                    : run_gram(p, x, gram, batch, p.m, p.n, &areas[0], stream);
+    if (st != MUON_POLAR_OK) return st;
+    st = run_poly(p, gram, poly, batch, b, c, &areas[1], stream);
+    if (st != MUON_POLAR_OK) return st;
+    return p.tall ? run_apply_r(p, poly, x, y, batch, p.m, p.n, a, &areas[2], stream)
+                  : run_apply(p, poly, x, y, batch, p.m, p.n, a, &areas[2], stream);
+}
+
+int reject_tall_stage(int64_t m, int64_t n) {
+    if (m > n)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
+                    "the stage entry points expect m <= n (muon_polar_step runs m > n)");
+    return MUON_POLAR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -481,8 +578,10 @@ int muon_polar_gram(const void *x, void *gram, void *workspace, size_t workspace
                     int64_t batch, int64_t m, int64_t n, hipStream_t stream) {
     if (x == nullptr || gram == nullptr)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    int st = reject_tall_stage(m, n);
+    if (st != MUON_POLAR_OK) return st;
     Plan p{};
-    int st = get_plan(batch, m, n, p);
+    st = get_plan(batch, m, n, p);
     if (st != MUON_POLAR_OK) return st;
     if (!aligned16(gram)) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram must be 16-byte aligned");
     SkArea area{};
@@ -496,8 +595,10 @@ int muon_polar_poly(const void *gram, void *poly, void *workspace, size_t worksp
                     int64_t batch, int64_t m, int64_t n, double b, double c, hipStream_t stream) {
     if (gram == nullptr || poly == nullptr)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    int st = reject_tall_stage(m, n);
+    if (st != MUON_POLAR_OK) return st;
     Plan p{};
-    int st = get_plan(batch, m, n, p);
+    st = get_plan(batch, m, n, p);
     if (st != MUON_POLAR_OK) return st;
     if (!aligned16(gram) || !aligned16(poly))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram and poly must be 16-byte aligned");
@@ -513,8 +614,10 @@ int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
                      hipStream_t stream) {
     if (poly == nullptr || x == nullptr || y == nullptr)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    int st = reject_tall_stage(m, n);
+    if (st != MUON_POLAR_OK) return st;
     Plan p{};
-    int st = get_plan(batch, m, n, p);
+    st = get_plan(batch, m, n, p);
     if (st != MUON_POLAR_OK) return st;
     if (!aligned16(poly)) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "poly must be 16-byte aligned");
     SkArea area{};
@@ -533,6 +636,10 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
     if (st != MUON_POLAR_OK) return st;
     st = check_workspace(p, workspace, workspace_bytes);
     if (st != MUON_POLAR_OK) return st;
+    if (p.tall) {
+        st = check_tall(p, x, y);
+        if (st != MUON_POLAR_OK) return st;
+    }
     void *gram = workspace;
     void *poly = static_cast<char *>(workspace) + align256(p.gram_bytes);
     if (p.sk_any) {
@@ -545,13 +652,9 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
             stream, "counter reset");
         if (st != MUON_POLAR_OK) return st;
     }
-    const SkArea area_gram = sk_area(p, workspace, 0), area_poly = sk_area(p, workspace, 1),
-                 area_apply = sk_area(p, workspace, 2);
-    st = run_gram(p, x, gram, batch, m, n, &area_gram, stream);
-    if (st != MUON_POLAR_OK) return st;
-    st = run_poly(p, gram, poly, batch, b, c, &area_poly, stream);
-    if (st != MUON_POLAR_OK) return st;
-    return run_apply(p, poly, x, y, batch, m, n, a, &area_apply, stream);
+    const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
+                             sk_area(p, workspace, 2)};
+    return run_step(p, x, y, gram, poly, areas, batch, a, b, c, stream);
 }
 
 int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace_bytes,
@@ -576,6 +679,10 @@ int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace
     const uintptr_t bytes = static_cast<uintptr_t>(batch * m * n * 2);
     if (xb < yb + bytes && yb < xb + bytes)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "x and y must not overlap");
+    if (p.tall && steps > 0) {
+        st = check_tall(p, x, y);
+        if (st != MUON_POLAR_OK) return st;
+    }
 
     char *ws = static_cast<char *>(workspace);
     void *gram = ws;
@@ -605,17 +712,12 @@ int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace
                           stream, "counter reset");
         if (st != MUON_POLAR_OK) return st;
     }
-    const SkArea area_gram = sk_area(p, workspace, 0), area_poly = sk_area(p, workspace, 1),
-                 area_apply = sk_area(p, workspace, 2);
+    const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
+                             sk_area(p, workspace, 2)};
     for (int64_t i = 0; i < steps; ++i) {
-        const double a = coefficients[3 * i], b = coefficients[3 * i + 1],
-                     c = coefficients[3 * i + 2];
         uint16_t *next = iterate(i + 1);
-        st = run_gram(p, cur, gram, batch, m, n, &area_gram, stream);
-        if (st != MUON_POLAR_OK) return st;
-        st = run_poly(p, gram, poly, batch, b, c, &area_poly, stream);
-        if (st != MUON_POLAR_OK) return st;
-        st = run_apply(p, poly, cur, next, batch, m, n, a, &area_apply, stream);
+        st = run_step(p, cur, next, gram, poly, areas, batch, coefficients[3 * i],
+                      coefficients[3 * i + 1], coefficients[3 * i + 2], stream);
         if (st != MUON_POLAR_OK) return st;
         cur = next;
     }

@@ -35,12 +35,13 @@ __device__ __forceinline__ u32x2 pack4(const uint16_t (&h)[4]) {
 template <Stage S>
 __device__ __forceinline__ void epilogue_values(const f32x16 &acc, int q, const float (&e)[4],
                                                 const GemmArgs &g, uint16_t (&h)[4]) {
+    constexpr Stage E = StageTraits<S>::kEpilogue;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const float v = acc[4 * q + t];
-        if constexpr (S == Stage::Apply)
-            h[t] = f32_to_bf16_bits(fmaf(g.s_epi, e[t], v));  // a·X + P·X
-        else if constexpr (S == Stage::Poly)
+        if constexpr (E == Stage::Apply)
+            h[t] = f32_to_bf16_bits(fmaf(g.s_epi, e[t], v));  // a·X + P·X  (a·X + X·P)
+        else if constexpr (E == Stage::Poly)
             h[t] = f32_to_bf16_bits(fmaf(g.s_acc, v, g.s_epi * e[t]));  // b·A + c·A²
         else
             h[t] = f32_to_bf16_bits(v);

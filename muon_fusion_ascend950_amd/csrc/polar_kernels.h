@@ -7,7 +7,25 @@
 
 namespace muon_polar {
 
-enum class Stage : int { Gram = 0, Poly = 1, Apply = 2 };
+// The three stages of a step on X [m, n] with m <= n (A = X·Xᵀ, P = b·A + c·A·A,
+// Y = a·X + P·X), and the right-Gram forms for m > n: G = Xᵀ·X (GramT) and
+// Y = a·X + X·P (ApplyR), which need no transposed copy of X.
+enum class Stage : int { Gram = 0, Poly = 1, Apply = 2, GramT = 3, ApplyR = 4 };
+
+// Compile-time properties of a stage.
+template <Stage S>
+struct StageTraits {
+    // upper-triangle tiles of a symmetric output, mirrored (square tiles)
+    static constexpr bool kSymmetric = S == Stage::Gram || S == Stage::Poly || S == Stage::GramT;
+    // operand panels stored [K][rows] (N-contiguous), read with transposing LDS reads
+    static constexpr bool kRowNC = S == Stage::GramT;
+    static constexpr bool kColNC = S == Stage::Apply || S == Stage::GramT;
+    // the epilogue reads a tile of `epi` (A for poly, X for apply)
+    static constexpr bool kEpiOperand = S == Stage::Poly || S == Stage::Apply || S == Stage::ApplyR;
+    // epilogue arithmetic: gram (round), poly (b·A + c·acc) or apply (a·X + acc)
+    static constexpr Stage kEpilogue =
+        S == Stage::GramT ? Stage::Gram : (S == Stage::ApplyR ? Stage::Apply : S);
+};
 
 // Kernel arguments, passed by value (no device-side tiling buffer).
 // Element offsets inside one batch matrix are 32-bit (the host rejects matrices

@@ -162,6 +162,11 @@ hipError_t launch_gemm(Stage s, int bm, int bn, bool vec, const GemmArgs &g, int
         case Stage::Apply:
             return vec ? launch_by_tile<Stage::Apply, true>(bm, bn, g, grid, stream)
                        : launch_by_tile<Stage::Apply, false>(bm, bn, g, grid, stream);
+        case Stage::GramT:
+        case Stage::ApplyR:
+            // right-Gram stages exist only as DMA-fed kernels (the host never
+            // routes them here)
+            return hipErrorInvalidValue;
     }
     return hipErrorInvalidValue;
 }

@@ -97,7 +97,10 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     constexpr int WM = BM / 2, WN = BN / (NW / 2);
     constexpr int SM = WM / 32, SN = WN / 32;
     constexpr int kMfmaPerSlice = SM * SN;
-    static_assert(S == Stage::Apply || BM == BN, "triangular stages need square tiles");
+    using Tr = StageTraits<S>;
+    static_assert(!Tr::kSymmetric || BM == BN, "triangular stages need square tiles");
+    static_assert(!Tr::kRowNC || 512 % BM == 0, "N-contiguous panel rows must tile 1 KiB");
+    static_assert(!Tr::kColNC || 512 % BN == 0, "N-contiguous panel rows must tile 1 KiB");
 
     constexpr int kStages = Geo::kStages;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * Geo::kStageBytes / 2];
@@ -153,9 +156,9 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         const int bt = tlin / g.tiles_per_batch;
         const int t = tlin - bt * g.tiles_per_batch;
         int tm, tn;
-        if constexpr (S == Stage::Apply) {
+        if constexpr (!Tr::kSymmetric) {
             // Grouped order: runs of group_n column tiles, walked row by row, so the
-            // tiles an XCD holds at once share few P row-panels and X column-panels.
+            // tiles an XCD holds at once share few row- and column-operand panels.
             const int gn = g.group_n;
             const int span = gn * g.tiles_m;
             const int grp = t / span, r = t - grp * span;
@@ -173,26 +176,40 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         // -------------------------------------------------------- DMA geometry
         // Per-lane byte offsets of this wave's DMA chunks at K-step 0 (kOob if the
         // chunk's row/column lies outside the matrix).
-        constexpr int kBRowsPerInstr = 512 / BN;  // apply: K-rows of X per 1 KiB
-        constexpr int kBLanesPerRow = BN / 8;
+        // K-contiguous panel ([rows][64], 8 rows per 1 KiB instruction) or
+        // N-contiguous panel ([64][rows], 512 / rows K-rows per instruction).
+        constexpr int kARowsPerInstr = 512 / BM, kALanesPerRow = BM / 8;
+        constexpr int kBRowsPerInstr = 512 / BN, kBLanesPerRow = BN / 8;
         auto a_row = [&](int i) { return 8 * (wave * Geo::kLoadsA + i) + (lane >> 3); };
         auto a_chunk = [&](int i) { return (lane & 7) ^ kc_swz(a_row(i)); };
-        auto b_krow = [&](int i) {  // apply
+        auto a_krow = [&](int i) {  // N-contiguous row operand
+            return (wave * Geo::kLoadsA + i) * kARowsPerInstr + lane / kALanesPerRow;
+        };
+        auto b_krow = [&](int i) {  // N-contiguous column operand
             return (wave * Geo::kLoadsB + i) * kBRowsPerInstr + lane / kBLanesPerRow;
         };
-        auto b_row = [&](int i) { return 8 * (wave * Geo::kLoadsB + i) + (lane >> 3); };  // gram/poly
+        auto b_row = [&](int i) { return 8 * (wave * Geo::kLoadsB + i) + (lane >> 3); };
         auto b_chunk = [&](int i) { return (lane & 7) ^ kc_swz(b_row(i)); };
 
         uint32_t off_a[Geo::kLoadsA], off_b[Geo::kLoadsB];
 #pragma unroll
         for (int i = 0; i < Geo::kLoadsA; ++i) {
-            const int gr = row0 + a_row(i);
-            off_a[i] = gr < g.row_rows ? static_cast<uint32_t>((gr * g.ld_row + 8 * a_chunk(i)) * 2)
-                                       : kOob;
+            if constexpr (Tr::kRowNC) {
+                const int krow = a_krow(i);
+                const int c = (lane % kALanesPerRow) ^ nc_swz<BM>(krow);
+                const int col = row0 + 8 * c;
+                off_a[i] =
+                    col < g.row_rows ? static_cast<uint32_t>((krow * g.ld_row + col) * 2) : kOob;
+            } else {
+                const int gr = row0 + a_row(i);
+                off_a[i] = gr < g.row_rows
+                               ? static_cast<uint32_t>((gr * g.ld_row + 8 * a_chunk(i)) * 2)
+                               : kOob;
+            }
         }
 #pragma unroll
         for (int i = 0; i < Geo::kLoadsB; ++i) {
-            if constexpr (S == Stage::Apply) {
+            if constexpr (Tr::kColNC) {
                 const int krow = b_krow(i);
                 const int c = (lane % kBLanesPerRow) ^ nc_swz<BN>(krow);
                 const int col = col0 + 8 * c;
@@ -213,22 +230,31 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             return smem_base + slot * Geo::kStageBytes + Geo::kABytes +
                    (wave * Geo::kLoadsB + i) * 1024;
         };
+        auto a_step = [&](int k0) -> uint32_t {
+            return static_cast<uint32_t>((Tr::kRowNC ? k0 * g.ld_row : k0) * 2);
+        };
         auto b_step = [&](int k0) -> uint32_t {
-            return static_cast<uint32_t>((S == Stage::Apply ? k0 * g.ld_col : k0) * 2);
+            return static_cast<uint32_t>((Tr::kColNC ? k0 * g.ld_col : k0) * 2);
         };
         // DMA instruction d (0 .. kLoads-1) of K-step `step` into `slot`; `tail`
         // applies the K-extent masks (only the last K-step can be partial).
         auto dma_one = [&](int d, int step, int slot, bool tail) {
             const int k0 = step * kBK;
             if (d < Geo::kLoadsA) {
-                uint32_t v = off_a[d] + static_cast<uint32_t>(k0 * 2);
-                if (tail && k0 + 8 * a_chunk(d) >= g.row_k) v = kOob;
+                uint32_t v = off_a[d] + a_step(k0);
+                if (tail) {
+                    if constexpr (Tr::kRowNC) {
+                        if (k0 + a_krow(d) >= g.row_k) v = kOob;
+                    } else {
+                        if (k0 + 8 * a_chunk(d) >= g.row_k) v = kOob;
+                    }
+                }
                 dma_16B(rs_row, a_dst(slot, d), v);
             } else {
                 const int i = d - Geo::kLoadsA;
                 uint32_t v = off_b[i] + b_step(k0);
                 if (tail) {
-                    if constexpr (S == Stage::Apply) {
+                    if constexpr (Tr::kColNC) {
                         if (k0 + b_krow(i) >= g.col_k) v = kOob;
                     } else {
                         if (k0 + 8 * b_chunk(i) >= g.col_k) v = kOob;
@@ -261,11 +287,15 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
             const uint16_t *bs = as + Geo::kABytes / 2;
 #pragma unroll
-            for (int i = 0; i < SM; ++i)
-                fr[i] = frag_kc(as, wr * WM + i * 32 + (lane & 31), kk, lane);
+            for (int i = 0; i < SM; ++i) {
+                if constexpr (Tr::kRowNC)
+                    fr[i] = frag_nc_tr<BM>(as, wr * WM + i * 32 + ((lane >> 4) & 1) * 16, kk, lane);
+                else
+                    fr[i] = frag_kc(as, wr * WM + i * 32 + (lane & 31), kk, lane);
+            }
 #pragma unroll
             for (int j = 0; j < SN; ++j) {
-                if constexpr (S == Stage::Apply)
+                if constexpr (Tr::kColNC)
                     fc[j] = frag_nc_tr<BN>(bs, wc * WN + j * 32 + ((lane >> 4) & 1) * 16, kk, lane);
                 else
                     fc[j] = frag_kc(bs, wc * WN + j * 32 + (lane & 31), kk, lane);
@@ -448,9 +478,9 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         // -------------------------------------------------------- epilogue
         uint16_t *tile = smem;
         uint16_t *out = g.out + bt * g.sb_out;
-        const bool diag = (S != Stage::Apply) && (tm == tn);
+        const bool diag = Tr::kSymmetric && (tm == tn);
 
-        if constexpr (S != Stage::Gram) {
+        if constexpr (Tr::kEpiOperand) {
             // Epilogue operand tile (A for poly, X for apply) -> LDS, rows/cols outside
             // the matrix read as zero.
             const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
@@ -483,7 +513,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                     const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
                     u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
                     float e[4] = {0.f, 0.f, 0.f, 0.f};
-                    if constexpr (S != Stage::Gram) unpack4(*p, e);
+                    if constexpr (Tr::kEpiOperand) unpack4(*p, e);
                     uint16_t h[4];
                     epilogue_values<S>(acc[i][j], q, e, g, h);
                     *p = pack4(h);
@@ -497,7 +527,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         for (int idx = tid; idx < BM * kChunksPerRow; idx += kThreads) {
             const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
             const int gr = row0 + row, gc = col0 + 8 * c;
-            if constexpr (S == Stage::Apply) {
+            if constexpr (!Tr::kSymmetric) {
                 if (gr >= g.out_rows || gc >= g.out_cols) continue;
             }
             u32x4 v;
@@ -521,7 +551,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
 
         // Mirrored store (symmetric stages, off-diagonal tiles): row c of the
         // mirror tile is column c of this tile; consecutive threads walk along it.
-        if constexpr (S != Stage::Apply) {
+        if constexpr (Tr::kSymmetric) {
             if (!diag) {
                 constexpr int kMirrorChunks = BM / 8;  // 16-byte chunks per mirror row
                 for (int idx = tid; idx < BN * kMirrorChunks; idx += kThreads) {
@@ -562,10 +592,10 @@ hipError_t launch_stream_by_tile(int bm, int bn, int waves, const GemmArgs &g, i
     if (bm == 64 && bn == 64) return launch_stream_one<64, 64, S>(g, grid, waves, stream);
     if (bm == 128 && bn == 128) return launch_stream_one<128, 128, S>(g, grid, waves, stream);
     if (bm == 256 && bn == 256) return launch_stream_one<256, 256, S>(g, grid, waves, stream);
-    if constexpr (S != Stage::Apply) {
+    if constexpr (S == Stage::Gram || S == Stage::Poly) {
         if (bm == 192 && bn == 192) return launch_stream_one<192, 192, S>(g, grid, waves, stream);
     }
-    if constexpr (S == Stage::Apply) {
+    if constexpr (!StageTraits<S>::kSymmetric) {
         if (bm == 128 && bn == 256) return launch_stream_one<128, 256, S>(g, grid, waves, stream);
         if (bm == 256 && bn == 128) return launch_stream_one<256, 128, S>(g, grid, waves, stream);
     }
@@ -592,10 +622,10 @@ int occupancy_by_tile(int bm, int bn, int waves) {
     if (bm == 64 && bn == 64) return occupancy_one<64, 64, S>(waves);
     if (bm == 128 && bn == 128) return occupancy_one<128, 128, S>(waves);
     if (bm == 256 && bn == 256) return occupancy_one<256, 256, S>(waves);
-    if constexpr (S != Stage::Apply) {
+    if constexpr (S == Stage::Gram || S == Stage::Poly) {
         if (bm == 192 && bn == 192) return occupancy_one<192, 192, S>(waves);
     }
-    if constexpr (S == Stage::Apply) {
+    if constexpr (!StageTraits<S>::kSymmetric) {
         if (bm == 128 && bn == 256) return occupancy_one<128, 256, S>(waves);
         if (bm == 256 && bn == 128) return occupancy_one<256, 128, S>(waves);
     }
@@ -618,6 +648,10 @@ hipError_t launch_stream(Stage s, int bm, int bn, int waves, const GemmArgs &g,
             return launch_stream_by_tile<Stage::Poly>(bm, bn, waves, g, grid, stream);
         case Stage::Apply:
             return launch_stream_by_tile<Stage::Apply>(bm, bn, waves, g, grid, stream);
+        case Stage::GramT:
+            return launch_stream_by_tile<Stage::GramT>(bm, bn, waves, g, grid, stream);
+        case Stage::ApplyR:
+            return launch_stream_by_tile<Stage::ApplyR>(bm, bn, waves, g, grid, stream);
     }
     return hipErrorInvalidValue;
 }
@@ -630,6 +664,10 @@ int stream_blocks_per_cu(Stage s, int bm, int bn, int waves) {
             return occupancy_by_tile<Stage::Poly>(bm, bn, waves);
         case Stage::Apply:
             return occupancy_by_tile<Stage::Apply>(bm, bn, waves);
+        case Stage::GramT:
+            return occupancy_by_tile<Stage::GramT>(bm, bn, waves);
+        case Stage::ApplyR:
+            return occupancy_by_tile<Stage::ApplyR>(bm, bn, waves);
     }
     return 0;
 }

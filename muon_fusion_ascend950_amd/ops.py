@@ -52,7 +52,11 @@ def polar_express(x: torch.Tensor, coefficients=COEFFICIENTS, normalize: bool = 
         raise ValueError("nothing to do: no coefficients and normalize=False")
     squeeze_batch = x.ndim == 2
     work = x.unsqueeze(0) if squeeze_batch else x
-    transposed = work.size(-2) > work.size(-1)
+    tall = work.size(-2) > work.size(-1)
+    if tall and work.size(-1) % 8 == 0:  # right-Gram form, no transposed copies
+        out = torch.ops.muon_ascend950.polar_express(work, flat, bool(normalize))
+        return out.squeeze(0) if squeeze_batch else out
+    transposed = tall
     if transposed:
         work = work.mT.contiguous()
     out = torch.ops.muon_ascend950.polar_express(work, flat, bool(normalize))
@@ -65,13 +69,20 @@ def polar_step(x: torch.Tensor, a: float, b: float, c: float) -> torch.Tensor:
     """Run one Polar Express iteration and return a tensor with the same shape.
 
     ``x`` must be a BF16 ROCm (HIP) tensor with shape ``[M,N]`` or ``[B,M,N]``.
-    The wrapper handles ``M > N`` by transposing around the native operator.
+    ``M > N`` runs the right-Gram form (``N % 8 == 0``) or, otherwise, transposes
+    around the native operator as the reference's wrapper does (ops.py:26-32).
     Non-aligned dimensions are handled by masked edge tiles inside the kernels.
     """
     _check(x)
     squeeze_batch = x.ndim == 2
     work = x.unsqueeze(0) if squeeze_batch else x
-    transposed = work.size(-2) > work.size(-1)
+    tall = work.size(-2) > work.size(-1)
+    if tall and work.size(-1) % 8 == 0:
+        # M > N in the right-Gram form Y = a·X + X·(b·G + c·G²), G = XᵀX: the same
+        # step without the two transposed copies (equal to them bit for bit)
+        out = torch.ops.muon_ascend950.polar_step_tall(work, float(a), float(b), float(c))
+        return out.squeeze(0) if squeeze_batch else out
+    transposed = tall
     if transposed:
         work = work.mT.contiguous()
 

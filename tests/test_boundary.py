@@ -191,11 +191,39 @@ def test_query_sizes(batch, m, n):
     assert info.workspace_bytes % 256 == 0
 
 
-@pytest.mark.parametrize("batch,m,n", [(0, 4, 4), (1, 0, 4), (1, 4, 0), (1, 5, 4), (-1, 4, 4)])
+@pytest.mark.parametrize("batch,m,n", [(0, 4, 4), (1, 0, 4), (1, 4, 0), (-1, 4, 4)])
 def test_query_rejects_bad_shapes(batch, m, n):
     with pytest.raises(capi.CapiError) as err:
         capi.query(batch, m, n)
     assert err.value.status == capi.ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("m,n", [(5, 4), (700, 256), (14336, 4096)])
+def test_query_tall_sizes_the_right_gram(m, n):
+    """m > n: the Gram matrix is XᵀX, n x n, so the padding follows n and the
+    sizes equal those of the transposed shape."""
+    tall = capi.query(2, m, n)
+    wide = capi.query(2, n, m)
+    assert tall.padded_rows == wide.padded_rows and tall.padded_rows >= n
+    assert tall.gram_bytes == wide.gram_bytes
+    assert tall.express_workspace_bytes >= 2 * tall.gram_bytes + 2 * 2 * m * n
+
+
+def test_tall_step_needs_n_multiple_of_8():
+    lib = capi.load()
+    # non-null pointers are never dereferenced: the shape check fails first
+    st = lib.muon_polar_step(16, 16, 16, 1 << 30, 1, 20, 12, 1.0, 1.0, 1.0, None)
+    assert st == capi.ERR_INVALID_ARGUMENT
+    assert "n % 8 == 0" in lib.muon_polar_last_error().decode()
+
+
+def test_tall_stage_entries_are_rejected():
+    lib = capi.load()
+    for call in (lambda: lib.muon_polar_gram(16, 16, None, 0, 1, 24, 16, None),
+                 lambda: lib.muon_polar_poly(16, 16, None, 0, 1, 24, 16, 1.0, 1.0, None),
+                 lambda: lib.muon_polar_apply(16, 16, 16, None, 0, 1, 24, 16, 1.0, None)):
+        assert call() == capi.ERR_INVALID_ARGUMENT
+        assert "m <= n" in lib.muon_polar_last_error().decode()
 
 
 def test_query_rejects_oversized_matrix():
