@@ -9,8 +9,9 @@ reported in ``secondary``.
 Timing follows the driver contract (W untimed warm-up calls, then exactly K calls
 between two device synchronisations) — the reference's own method is the same loop
 (README.md:179-191).  Per-kernel durations come from HIP events recorded on the
-launch stream around each stage launched alone through the C ABI; ``roofline`` uses
-the dominant kernel (stage 3, P·X + a·X).
+launch stream between the stages of a step sequence launched through the C ABI (so each
+stage sees the caches as inside a step); ``roofline`` uses the dominant kernel (stage 3,
+P·X + a·X).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -83,11 +84,13 @@ def kernel_us(fn, launches: int, warmup: int = 3) -> float:
     return start.elapsed_time(stop) * 1e3 / launches
 
 
-def stage_times(batch: int, m: int, n: int, launches: int):
-    """µs per launch of each stage, each launched alone on torch's current stream,
-    with polar_step's workspace (A and P in it, and the same stream-K split as in
-    the step; a stage call with a workspace also clears its arrival counters, a
-    one-block fill kernel included in its time)."""
+def stage_times(batch: int, m: int, n: int, launches: int, warmup: int = 3):
+    """µs per launch of each stage as it runs inside a step: gram, poly and apply are
+    launched in step order through the C ABI with polar_step's workspace (A and P in
+    it, the same stream-K split as in the step), `launches` times, with HIP events on
+    torch's current stream (the launch stream) between the stages; each stage's time is
+    the sum of its event intervals / launches.  A stage call given a workspace clears
+    its own arrival counters (a one-block fill kernel, inside its interval)."""
     import torch
     from muon_fusion_ascend950_amd import capi
 
@@ -99,14 +102,23 @@ def stage_times(batch: int, m: int, n: int, launches: int):
     poly = ws[p_off:p_off + info.gram_bytes].view(torch.bfloat16).view(batch, mp, mp)
     y = torch.empty_like(x)
     a, b, c = COEFFS
-    capi.gram(x, gram, workspace=ws)
-    capi.poly(gram, poly, batch, m, n, b, c, workspace=ws)
-    return {
-        "gram": kernel_us(lambda: capi.gram(x, gram, workspace=ws), launches),
-        "poly": kernel_us(lambda: capi.poly(gram, poly, batch, m, n, b, c, workspace=ws),
-                          launches),
-        "apply": kernel_us(lambda: capi.apply(poly, x, y, a, workspace=ws), launches),
-    }
+    stages = (("gram", lambda: capi.gram(x, gram, workspace=ws)),
+              ("poly", lambda: capi.poly(gram, poly, batch, m, n, b, c, workspace=ws)),
+              ("apply", lambda: capi.apply(poly, x, y, a, workspace=ws)))
+    for _ in range(warmup):
+        for _, fn in stages:
+            fn()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
+              for _ in range(launches)]
+    for ev in events:
+        ev[0].record()
+        for i, (_, fn) in enumerate(stages):
+            fn()
+            ev[i + 1].record()
+    torch.cuda.synchronize()
+    return {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in events) * 1e3 / launches
+            for i, (name, _) in enumerate(stages)}
 
 
 def torch_eager(x):
@@ -118,6 +130,37 @@ def torch_eager(x):
     a, b, c = COEFFS
     gram = torch.matmul(x, x.mT.contiguous())
     return a * x + torch.matmul(b * gram + c * torch.matmul(gram, gram), x)
+
+
+MUON_LR, MUON_MOMENTUM, MUON_WD = 0.02, 0.95, 0.01
+
+
+def muon_tensors(m: int, n: int):
+    """fp32 parameter, gradient and momentum buffer of one [m, n] matrix on the GPU."""
+    import torch
+
+    gen = torch.Generator().manual_seed(2)
+    p = (torch.randn(m, n, generator=gen) * 0.02).cuda()
+    g = (torch.randn(m, n, generator=gen) * 1e-3).cuda()
+    buf = (torch.randn(m, n, generator=gen) * 1e-3).cuda()
+    return p, g, buf
+
+
+def muon_eager_step(p, g, buf, coefficients):
+    """nanochat's Muon step in plain PyTorch on the GPU (momentum lerps, bf16 Polar
+    Express with the reference recipe's normalisation, decoupled decay, shape-scaled
+    add): the comparison point of the native update."""
+    import torch
+
+    buf.lerp_(g, 1 - MUON_MOMENTUM)
+    u = g.lerp(buf, MUON_MOMENTUM)
+    x = u.bfloat16()
+    x = x / (x.norm(dim=(-2, -1), keepdim=True) * 1.01 + 1e-6)
+    for a, b, c in coefficients:
+        gram = torch.matmul(x, x.mT.contiguous())
+        x = a * x + torch.matmul(b * gram + c * torch.matmul(gram, gram), x)
+    p.mul_(1 - MUON_LR * MUON_WD)
+    p.add_(x, alpha=-MUON_LR * max(1.0, p.size(-2) / p.size(-1)) ** 0.5)
 
 
 def read_traffic():
@@ -167,6 +210,9 @@ def main() -> int:
     ap.add_argument("--profile", action="store_true",
                     help="only the headline step loop and three 1 GiB device copies (the "
                          "calibration kernel of known size), for rocprofv3 runs")
+    ap.add_argument("--profile-muon", action="store_true",
+                    help="only a loop of Muon updates of one fp32 [4096,14336] parameter, "
+                         "for rocprofv3 runs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -184,6 +230,13 @@ def main() -> int:
 
     # ---- headline: [4096,14336], one step
     batch, m, n = HEADLINE
+    if args.profile_muon:
+        p, g, buf = muon_tensors(m, n)
+        sec = time_calls(lambda: mf.muon_update(p, g, buf, lr=MUON_LR, momentum=MUON_MOMENTUM,
+                                                weight_decay=MUON_WD), args.steps, args.warmup)
+        print(json.dumps({"profile": "muon_update fp32 [4096,14336]", "steps": args.steps,
+                          "us_per_update": round(sec * 1e6, 2)}), flush=True)
+        return 0
     x = make_input((m, n), seed=0).cuda()
     if args.profile:
         sec = time_calls(lambda: mf.polar_step(x, a, b, c), args.steps, args.warmup)
@@ -223,6 +276,14 @@ def main() -> int:
     raw = raw.cuda()
     sec_express = time_calls(lambda: mf.polar_express(raw), 10, 3)
     sec_loop = time_calls(reference_loop, 10, 3)
+
+    # Muon update of one fp32 [4096,14336] parameter: the native update (momentum pass,
+    # normalisation, 5 steps, parameter update) vs nanochat's step in PyTorch eager
+    p, g, buf = muon_tensors(m, n)
+    sec_muon = time_calls(lambda: mf.muon_update(p, g, buf, lr=MUON_LR, momentum=MUON_MOMENTUM,
+                                                 weight_decay=MUON_WD), 10, 3)
+    sec_muon_eager = time_calls(lambda: muon_eager_step(p, g, buf, mf.COEFFICIENTS), 5, 2)
+    del p, g, buf
 
     # PyTorch eager on the same GPU (the reference's comparison point, README.md:172-208)
     eager = time_calls(lambda: torch_eager(x), 10, 3)
@@ -267,6 +328,14 @@ def main() -> int:
             "polar_express_us": round(sec_express * 1e6, 2),
             "torch_norm_plus_5_polar_step_us": round(sec_loop * 1e6, 2),
             "tflops": round(5 * flops / sec_express / 1e12, 2),
+        },
+        "muon_update": {
+            "workload": ("Muon update of one fp32 [4096,14336] parameter: Nesterov momentum, "
+                         "normalise + 5 steps (bf16), decoupled weight decay, shape-scaled step"),
+            "native_us": round(sec_muon * 1e6, 2),
+            "torch_eager_us": round(sec_muon_eager * 1e6, 2),
+            "speedup_vs_torch_eager": round(sec_muon_eager / sec_muon, 3),
+            "elementwise_us": round((sec_muon - sec_express) * 1e6, 2),
         },
         "secondary": {
             "workload": "polar_step on bf16 [8,512,2048], one step",

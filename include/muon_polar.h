@@ -70,6 +70,8 @@ typedef struct muon_polar_shape_info {
     size_t workspace_bytes; /* bytes for A and P (each 256-byte aligned) and the stream-K area */
     size_t express_workspace_bytes; /* muon_polar_express: the above, one [batch, m, n] bf16
                                        buffer and the normalisation partial sums */
+    size_t muon_workspace_bytes;    /* muon_polar_muon_update: the above and one more
+                                       [batch, m, n] bf16 buffer */
 } muon_polar_shape_info;
 
 int muon_polar_query(int64_t batch, int64_t m, int64_t n, muon_polar_shape_info *info);
@@ -125,6 +127,32 @@ int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
 int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace_bytes,
                        int64_t batch, int64_t m, int64_t n, const double *coefficients,
                        int64_t steps, int normalize, hipStream_t stream);
+
+/* Muon optimizer update of one parameter (or a batch of equally shaped ones):
+ * param, grad and momentum_buffer are fp32 [batch, m, n], row-major contiguous,
+ * pairwise disjoint and disjoint from the workspace.
+ *
+ *     buf ← lerp(buf, grad, 1 − momentum)
+ *     g'  = nesterov ? lerp(grad, buf, momentum) : buf
+ *     O   = muon_polar_express(bf16(g'), coefficients, steps, normalize = 1)
+ *     param ← param·(1 − lr·weight_decay) − (lr·lr_scale)·O
+ *
+ * lerp is torch.lerp's two-branch form (start + w·(end − start) for |w| < 0.5,
+ * else end − (end − start)·(1 − w)), every fp32 operation rounded on its own;
+ * the scalars are rounded to fp32 as (float)(1 − momentum), (float)momentum,
+ * (float)(1 − lr·weight_decay) and (float)(−lr·lr_scale).  lr_scale is the
+ * caller's shape factor (nanochat's Muon: sqrt(max(1, rows / cols)) of the
+ * parameter).  m > n needs n % 8 == 0 (right-Gram form).  `workspace` must hold
+ * info.muon_workspace_bytes.  grad is read only; buf and param are updated in
+ * place.
+ * No reference counterpart: the reference provides the orthogonalisation only
+ * and leaves momentum, weight decay and the parameter update to its caller
+ * (README.md:130; the caller is nanochat's Muon optimizer, README.md:247). */
+int muon_polar_muon_update(void *param, const void *grad, void *momentum_buffer,
+                           void *workspace, size_t workspace_bytes, int64_t batch, int64_t m,
+                           int64_t n, double momentum, int nesterov, const double *coefficients,
+                           int64_t steps, double lr, double weight_decay, double lr_scale,
+                           hipStream_t stream);
 
 /* Detail of the last failure on the calling thread ("" if none).
  * Replaces CheckAcl / aclGetRecentErrMsg (csrc/muon_polar_step_binding.cpp:72-75). */

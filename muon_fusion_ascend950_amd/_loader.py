@@ -60,9 +60,14 @@ def load_library() -> None:
     def fake_polar_express(x, coefficients, normalize: bool):
         return torch.empty_like(x, memory_format=torch.contiguous_format)
 
+    def fake_muon_update(param, grad, momentum_buffer, momentum, nesterov, coefficients, lr,
+                         weight_decay, lr_scale):
+        return None
+
     for name, fake in (("muon_ascend950::polar_step", fake_polar_step),
                        ("muon_ascend950::polar_step_tall", fake_polar_step),
-                       ("muon_ascend950::polar_express", fake_polar_express)):
+                       ("muon_ascend950::polar_express", fake_polar_express),
+                       ("muon_ascend950::muon_update", fake_muon_update)):
         try:
             torch.library.register_fake(name)(fake)
         except RuntimeError as exc:

@@ -19,6 +19,7 @@ EXPORTED_FUNCTIONS = (
     "muon_polar_poly",
     "muon_polar_apply",
     "muon_polar_express",
+    "muon_polar_muon_update",
     "muon_polar_last_error",
     "muon_polar_version",
 )
@@ -36,6 +37,7 @@ class ShapeInfo(ctypes.Structure):
         ("gram_bytes", ctypes.c_size_t),
         ("workspace_bytes", ctypes.c_size_t),
         ("express_workspace_bytes", ctypes.c_size_t),
+        ("muon_workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -75,8 +77,11 @@ def load() -> ctypes.CDLL:
     lib.muon_polar_apply.argtypes = [vp, vp, vp, vp, sz, i64, i64, i64, dbl, vp]
     lib.muon_polar_express.argtypes = [vp, vp, vp, sz, i64, i64, i64,
                                        ctypes.POINTER(ctypes.c_double), i64, ctypes.c_int, vp]
+    lib.muon_polar_muon_update.argtypes = [vp, vp, vp, vp, sz, i64, i64, i64, dbl, ctypes.c_int,
+                                           ctypes.POINTER(ctypes.c_double), i64, dbl, dbl, dbl,
+                                           vp]
     for name in ("muon_polar_query", "muon_polar_step", "muon_polar_gram", "muon_polar_poly",
-                 "muon_polar_apply", "muon_polar_express"):
+                 "muon_polar_apply", "muon_polar_express", "muon_polar_muon_update"):
         getattr(lib, name).restype = ctypes.c_int
     lib.muon_polar_last_error.argtypes = []
     lib.muon_polar_last_error.restype = ctypes.c_char_p
@@ -172,3 +177,24 @@ def apply(poly_buf, x, y, a: float, stream=None, workspace=None) -> None:
     check("muon_polar_apply", load().muon_polar_apply(
         poly_buf.data_ptr(), x.data_ptr(), y.data_ptr(), *_ws(workspace), batch, m, n,
         float(a), _stream(stream)))
+
+
+def alloc_muon_workspace(batch: int, m: int, n: int, device="cuda"):
+    import torch
+
+    info = query(batch, m, n)
+    return torch.empty(info.muon_workspace_bytes, dtype=torch.uint8, device=device), info
+
+
+def muon_update(param, grad, momentum_buffer, workspace, coefficients, *, momentum: float,
+                nesterov: bool, lr: float, weight_decay: float, lr_scale: float,
+                stream=None) -> None:
+    """muon_polar_muon_update on fp32 [batch, m, n] tensors (param and buffer in place)."""
+    batch, m, n = _bmn(param)
+    flat = [float(v) for triple in coefficients for v in triple]
+    arr = (ctypes.c_double * max(1, len(flat)))(*flat)
+    check("muon_polar_muon_update", load().muon_polar_muon_update(
+        param.data_ptr(), grad.data_ptr(), momentum_buffer.data_ptr(), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), batch, m, n, float(momentum),
+        int(bool(nesterov)), arr, len(flat) // 3, float(lr), float(weight_decay), float(lr_scale),
+        _stream(stream)))

@@ -121,16 +121,56 @@ at::Tensor MuonPolarExpressHip(const at::Tensor &x, at::ArrayRef<double> coeffic
     return out;
 }
 
+// Muon update of param (in place) and momentum_buffer (in place) from grad; no
+// reference counterpart (the reference leaves the update to its caller,
+// README.md:130).  All three fp32 [batch, M, N], contiguous, on one device.
+void MuonUpdateHip(const at::Tensor &param, const at::Tensor &grad,
+                   const at::Tensor &momentum_buffer, double momentum, bool nesterov,
+                   at::ArrayRef<double> coefficients, double lr, double weight_decay,
+                   double lr_scale) {
+    for (const at::Tensor *t : {&param, &grad, &momentum_buffer}) {
+        TORCH_CHECK(t->defined(), "muon_update: tensors must be defined");
+        TORCH_CHECK(t->device().is_cuda(), "muon_update: tensors must be ROCm (HIP) device tensors");
+        TORCH_CHECK(t->device() == param.device(), "muon_update: tensors must share one device");
+        TORCH_CHECK(t->scalar_type() == at::kFloat, "muon_update: param, grad and momentum_buffer must be float32");
+        TORCH_CHECK(t->sizes() == param.sizes(), "muon_update: param, grad and momentum_buffer must have one shape");
+    }
+    TORCH_CHECK(param.dim() == 3, "muon_update: tensors must have shape [batch, M, N]");
+    TORCH_CHECK(param.size(0) > 0 && param.size(1) > 0 && param.size(2) > 0,
+                "muon_update: all dimensions must be positive");
+    TORCH_CHECK(param.is_contiguous() && momentum_buffer.is_contiguous(),
+                "muon_update: param and momentum_buffer must be contiguous (they are updated in place)");
+    TORCH_CHECK(coefficients.size() % 3 == 0, "muon_update: coefficients must be (a, b, c) triples");
+    const c10::OptionalDeviceGuard device_guard(param.device());
+    const at::Tensor g = grad.contiguous();
+    const int64_t batch = param.size(0), m = param.size(1), n = param.size(2);
+    muon_polar_shape_info info{};
+    int st = muon_polar_query(batch, m, n, &info);
+    TORCH_CHECK(st == MUON_POLAR_OK, "muon_update: ", muon_polar_last_error());
+    at::Tensor workspace = at::empty({static_cast<int64_t>(info.muon_workspace_bytes)},
+                                     param.options().dtype(at::kByte));
+    hipStream_t stream = c10::hip::getCurrentHIPStream(param.device().index()).stream();
+    st = muon_polar_muon_update(param.data_ptr(), g.data_ptr(), momentum_buffer.data_ptr(),
+                                workspace.data_ptr(), info.muon_workspace_bytes, batch, m, n,
+                                momentum, nesterov ? 1 : 0, coefficients.data(),
+                                static_cast<int64_t>(coefficients.size() / 3), lr, weight_decay,
+                                lr_scale, stream);
+    TORCH_CHECK(st == MUON_POLAR_OK, "muon_update: ", muon_polar_last_error());
+}
+
 }  // namespace
 
 TORCH_LIBRARY(muon_ascend950, m) {
     m.def("polar_step(Tensor x, float a, float b, float c) -> Tensor");
     m.def("polar_step_tall(Tensor x, float a, float b, float c) -> Tensor");
     m.def("polar_express(Tensor x, float[] coefficients, bool normalize) -> Tensor");
+    m.def("muon_update(Tensor(a!) param, Tensor grad, Tensor(b!) momentum_buffer, float momentum, "
+          "bool nesterov, float[] coefficients, float lr, float weight_decay, float lr_scale) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(muon_ascend950, CUDA, m) {
     m.impl("polar_step", &MuonPolarStepHip);
     m.impl("polar_step_tall", &MuonPolarStepTallHip);
     m.impl("polar_express", &MuonPolarExpressHip);
+    m.impl("muon_update", &MuonUpdateHip);
 }

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -122,6 +123,7 @@ struct Plan {
     // muon_polar_express: one [batch, m, n] bf16 buffer, then the normalisation
     // partial sums, after the step's workspace
     size_t express_x_offset, express_norm_offset, express_workspace_bytes;
+    size_t muon_o_offset, muon_workspace_bytes;  // muon_polar_muon_update: + O [batch, m, n] bf16
 };
 
 std::mutex g_plan_mutex;
@@ -309,6 +311,8 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.express_workspace_bytes =
         p.express_norm_offset +
         align256(size_t(batch) * muon_polar::norm_chunks(m * n) * sizeof(float));
+    p.muon_o_offset = p.express_workspace_bytes;
+    p.muon_workspace_bytes = p.muon_o_offset + align256(size_t(batch) * m * n * 2u);
     g_plans.emplace(key, p);
     out = p;
     return MUON_POLAR_OK;
@@ -551,6 +555,36 @@ int run_step(const Plan &p, const void *x, void *y, void *gram, void *poly, cons
                   : run_apply(p, poly, x, y, batch, p.m, p.n, a, &areas[2], stream);
 }
 
+// `steps` steps from `cur` (the normalised input, in the chain's first buffer),
+// alternating between `out` and `scratch` so that the last step writes `out`.
+int run_steps(const Plan &p, void *workspace, const uint16_t *cur, uint16_t *out,
+              uint16_t *scratch, int64_t batch, const double *coefficients, int64_t steps,
+              hipStream_t stream) {
+    if (steps == 0) return MUON_POLAR_OK;
+    char *ws = static_cast<char *>(workspace);
+    if (p.sk_any) {
+        // The stage kernels leave every counter they use at zero, so one clear
+        // covers all steps.
+        const int st = finish_stage(
+            muon_polar::launch_zero_words(reinterpret_cast<uint32_t *>(ws + p.counters_offset),
+                                          3 * p.counter_stride, stream),
+            stream, "counter reset");
+        if (st != MUON_POLAR_OK) return st;
+    }
+    void *gram = ws;
+    void *poly = ws + align256(p.gram_bytes);
+    const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
+                             sk_area(p, workspace, 2)};
+    for (int64_t i = 0; i < steps; ++i) {
+        uint16_t *next = (steps - i - 1) % 2 == 0 ? out : scratch;
+        const int st = run_step(p, cur, next, gram, poly, areas, batch, coefficients[3 * i],
+                                coefficients[3 * i + 1], coefficients[3 * i + 2], stream);
+        if (st != MUON_POLAR_OK) return st;
+        cur = next;
+    }
+    return MUON_POLAR_OK;
+}
+
 int reject_tall_stage(int64_t m, int64_t n) {
     if (m > n)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
@@ -571,6 +605,7 @@ int muon_polar_query(int64_t batch, int64_t m, int64_t n, muon_polar_shape_info 
     info->gram_bytes = p.gram_bytes;
     info->workspace_bytes = p.workspace_bytes;
     info->express_workspace_bytes = p.express_workspace_bytes;
+    info->muon_workspace_bytes = p.muon_workspace_bytes;
     return MUON_POLAR_OK;
 }
 
@@ -685,8 +720,6 @@ int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace
     }
 
     char *ws = static_cast<char *>(workspace);
-    void *gram = ws;
-    void *poly = ws + align256(p.gram_bytes);
     uint16_t *scratch = reinterpret_cast<uint16_t *>(ws + p.express_x_offset);
     float *partial = reinterpret_cast<float *>(ws + p.express_norm_offset);
     uint16_t *out = static_cast<uint16_t *>(y);
@@ -703,25 +736,79 @@ int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace
         if (st != MUON_POLAR_OK) return st;
         cur = dst;
     }
-    if (steps > 0 && p.sk_any) {
-        // The stage kernels leave every counter they use at zero, so one clear
-        // covers all steps.
-        st = finish_stage(muon_polar::launch_zero_words(
-                              reinterpret_cast<uint32_t *>(ws + p.counters_offset),
-                              3 * p.counter_stride, stream),
-                          stream, "counter reset");
+    return run_steps(p, workspace, cur, out, scratch, batch, coefficients, steps, stream);
+}
+
+int muon_polar_muon_update(void *param, const void *grad, void *momentum_buffer,
+                           void *workspace, size_t workspace_bytes, int64_t batch, int64_t m,
+                           int64_t n, double momentum, int nesterov, const double *coefficients,
+                           int64_t steps, double lr, double weight_decay, double lr_scale,
+                           hipStream_t stream) {
+    if (param == nullptr || grad == nullptr || momentum_buffer == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    if (steps < 0) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "steps must be >= 0");
+    if (steps > 0 && coefficients == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "coefficients is null");
+    if (!std::isfinite(momentum) || momentum < 0.0 || momentum > 1.0)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "momentum must be in [0, 1]");
+    if (!std::isfinite(lr) || !std::isfinite(weight_decay) || !std::isfinite(lr_scale))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "lr, weight_decay and lr_scale must be finite");
+    Plan p{};
+    int st = get_plan(batch, m, n, p);
+    if (st != MUON_POLAR_OK) return st;
+    if (workspace == nullptr || workspace_bytes < p.muon_workspace_bytes)
+        return fail(MUON_POLAR_ERR_WORKSPACE,
+                    "workspace must hold " + std::to_string(p.muon_workspace_bytes) +
+                        " bytes, got " + std::to_string(workspace == nullptr ? 0 : workspace_bytes));
+    if (!aligned16(workspace))
+        return fail(MUON_POLAR_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+    // fp32 param, grad and buffer, and the workspace: pairwise disjoint
+    const uintptr_t f32_bytes = static_cast<uintptr_t>(batch * m * n * 4);
+    const uintptr_t lo[4] = {reinterpret_cast<uintptr_t>(param), reinterpret_cast<uintptr_t>(grad),
+                             reinterpret_cast<uintptr_t>(momentum_buffer),
+                             reinterpret_cast<uintptr_t>(workspace)};
+    const uintptr_t len[4] = {f32_bytes, f32_bytes, f32_bytes,
+                              static_cast<uintptr_t>(p.muon_workspace_bytes)};
+    for (int i = 0; i < 4; ++i)
+        for (int j = i + 1; j < 4; ++j)
+            if (lo[i] < lo[j] + len[j] && lo[j] < lo[i] + len[i])
+                return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
+                            "param, grad, momentum_buffer and workspace must not overlap");
+
+    char *ws = static_cast<char *>(workspace);
+    uint16_t *out = reinterpret_cast<uint16_t *>(ws + p.muon_o_offset);
+    uint16_t *scratch = reinterpret_cast<uint16_t *>(ws + p.express_x_offset);
+    if (p.tall && steps > 0) {
+        st = check_tall(p, out, scratch);
         if (st != MUON_POLAR_OK) return st;
     }
-    const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
-                             sk_area(p, workspace, 2)};
-    for (int64_t i = 0; i < steps; ++i) {
-        uint16_t *next = iterate(i + 1);
-        st = run_step(p, cur, next, gram, poly, areas, batch, coefficients[3 * i],
-                      coefficients[3 * i + 1], coefficients[3 * i + 2], stream);
-        if (st != MUON_POLAR_OK) return st;
-        cur = next;
-    }
-    return MUON_POLAR_OK;
+    float *partial = reinterpret_cast<float *>(ws + p.express_norm_offset);
+    // The normalised input goes where the iterate chain starts (out for an even
+    // step count, else scratch); the momentum pass writes the other buffer, which
+    // the first step overwrites only after the normalisation has read it.
+    uint16_t *first = steps % 2 == 0 ? out : scratch;
+    uint16_t *x0 = steps % 2 == 0 ? scratch : out;
+    const int64_t mn = m * n;
+    const bool vec = mn % 8 == 0 && aligned16(grad) && aligned16(momentum_buffer);
+    st = finish_stage(
+        muon_polar::launch_muon_momentum(static_cast<const float *>(grad),
+                                         static_cast<float *>(momentum_buffer), x0, partial, batch,
+                                         mn, static_cast<float>(1.0 - momentum),
+                                         static_cast<float>(momentum), nesterov != 0, vec, stream),
+        stream, "momentum");
+    if (st != MUON_POLAR_OK) return st;
+    st = finish_stage(muon_polar::launch_norm_scale(x0, first, partial, batch, mn, mn % 8 == 0,
+                                                    stream),
+                      stream, "normalize");
+    if (st != MUON_POLAR_OK) return st;
+    st = run_steps(p, workspace, first, out, scratch, batch, coefficients, steps, stream);
+    if (st != MUON_POLAR_OK) return st;
+    const int64_t total = batch * mn;
+    return finish_stage(
+        muon_polar::launch_muon_param_update(
+            static_cast<float *>(param), out, total, static_cast<float>(1.0 - lr * weight_decay),
+            static_cast<float>(-lr * lr_scale), total % 8 == 0 && aligned16(param), stream),
+        stream, "param update");
 }
 
 const char *muon_polar_last_error(void) { return g_last_error.c_str(); }

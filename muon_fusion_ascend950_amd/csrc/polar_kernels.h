@@ -92,5 +92,19 @@ constexpr int64_t kNormChunk = 256 * 8 * 32;  // elements per partial sum
 int64_t norm_chunks(int64_t mn);
 hipError_t launch_normalize(const uint16_t *x, uint16_t *y, float *partial, int64_t batch,
                             int64_t mn, bool vec, hipStream_t stream);
+// The scale pass alone, from partial sums already in `partial`.
+hipError_t launch_norm_scale(const uint16_t *x, uint16_t *y, const float *partial,
+                             int64_t batch, int64_t mn, bool vec, hipStream_t stream);
+
+// Muon update passes (polar_norm.hip).  Momentum: buf ← lerp(buf, g, w),
+// g' = nesterov ? lerp(g, buf, beta) : buf, x0 = bf16(g'), and x0's per-chunk
+// sums of squares into `partial` in launch_normalize's order (ready for
+// launch_norm_scale).  vec: mn % 8 == 0 and 16-byte aligned g, buf, x0.
+hipError_t launch_muon_momentum(const float *g, float *buf, uint16_t *x0, float *partial,
+                                int64_t batch, int64_t mn, float w, float beta, bool nesterov,
+                                bool vec, hipStream_t stream);
+// p ← p·decay + alpha·O over `total` elements; vec: total % 8 == 0, 16-byte aligned.
+hipError_t launch_muon_param_update(float *p, const uint16_t *o, int64_t total, float decay,
+                                    float alpha, bool vec, hipStream_t stream);
 
 }  // namespace muon_polar

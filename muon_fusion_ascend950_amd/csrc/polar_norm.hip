@@ -11,6 +11,11 @@
 // scale pass in which every block re-sums its matrix's partials in the same
 // fixed order (so all blocks of a matrix agree, and results are run-to-run
 // identical).
+//
+// Also the two element-wise passes of the Muon update around the iteration:
+// the momentum pass (fp32 momentum buffer and Nesterov blend, the bf16 input of
+// the iteration and its sums of squares in the normalisation's own order) and
+// the parameter update p = p·(1 − lr·wd) − lr·scale·O.
 #include "polar_kernels.h"
 #include "polar_tile.hpp"
 
@@ -104,9 +109,161 @@ __global__ __launch_bounds__(kNormThreads) void norm_scale_kernel(const uint16_t
     }
 }
 
+// torch.lerp's two-branch form (ATen Lerp.h): start + w·(end − start) for |w| < 0.5,
+// else end − (end − start)·(1 − w); every operation rounded on its own.
+__device__ __forceinline__ float lerp_rounded(float start, float end, float w) {
+#pragma clang fp contract(off)
+    return fabsf(w) < 0.5f ? start + w * (end - start) : end - (end - start) * (1.0f - w);
+}
+
+// Momentum pass of the Muon update over chunk c of matrix b (chunks as in
+// norm_partial_kernel):
+//     buf ← lerp(buf, g, w)                  (w = 1 − momentum)
+//     g'  = lerp(g, buf, momentum) | buf     (Nesterov or plain)
+//     x0  = bf16(g'),   partial[b, c] = Σ x0²  in norm_partial_kernel's order
+// order8: mn % 8 == 0 (8 consecutive elements per thread and step, the vector
+// path's order); vec: also 16-byte aligned g, buf and x0 (vector accesses).
+template <bool kOrder8, bool kVec>
+__global__ __launch_bounds__(kNormThreads) void muon_momentum_kernel(
+    const float *__restrict__ g, float *__restrict__ buf, uint16_t *__restrict__ x0,
+    float *__restrict__ partial, int64_t mn, int chunks, float w, float beta, int nesterov) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    const int b = blockIdx.x / chunks, c = blockIdx.x - b * chunks;
+    const int64_t base = int64_t(b) * mn;
+    const int64_t e0 = int64_t(c) * kNormChunk;
+    const int64_t e1 = e0 + kNormChunk < mn ? e0 + kNormChunk : mn;
+    float acc = 0.0f;
+    auto one = [&](float gv, float bv, uint32_t &h) {
+        const float nb = lerp_rounded(bv, gv, w);
+        const float u = nesterov ? lerp_rounded(gv, nb, beta) : nb;
+        h = f32_to_bf16_bits(u);
+        const float r = bf16_bits_to_f32(h);
+        acc = fmaf(r, r, acc);
+        return nb;
+    };
+    if (kOrder8) {
+        for (int64_t e = e0 + threadIdx.x * 8; e < e1; e += kNormThreads * 8) {
+            float gv[8], bv[8];
+            if (kVec) {
+                const f32x4 g0 = *reinterpret_cast<const f32x4 *>(g + base + e);
+                const f32x4 g1 = *reinterpret_cast<const f32x4 *>(g + base + e + 4);
+                const f32x4 b0 = *reinterpret_cast<const f32x4 *>(buf + base + e);
+                const f32x4 b1 = *reinterpret_cast<const f32x4 *>(buf + base + e + 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    gv[i] = g0[i]; gv[i + 4] = g1[i];
+                    bv[i] = b0[i]; bv[i + 4] = b1[i];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    gv[i] = g[base + e + i];
+                    bv[i] = buf[base + e + i];
+                }
+            }
+            float nb[8];
+            uint32_t h[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) nb[i] = one(gv[i], bv[i], h[i]);
+            if (kVec) {
+                *reinterpret_cast<f32x4 *>(buf + base + e) = f32x4{nb[0], nb[1], nb[2], nb[3]};
+                *reinterpret_cast<f32x4 *>(buf + base + e + 4) = f32x4{nb[4], nb[5], nb[6], nb[7]};
+                *reinterpret_cast<u32x4 *>(x0 + base + e) =
+                    u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                          h[6] | (h[7] << 16)};
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    buf[base + e + i] = nb[i];
+                    x0[base + e + i] = static_cast<uint16_t>(h[i]);
+                }
+            }
+        }
+    } else {
+        for (int64_t e = e0 + threadIdx.x; e < e1; e += kNormThreads) {
+            uint32_t h;
+            buf[base + e] = one(g[base + e], buf[base + e], h);
+            x0[base + e] = static_cast<uint16_t>(h);
+        }
+    }
+    const float t = block_sum(acc, red);
+    if (threadIdx.x == 0) partial[blockIdx.x] = t;
+}
+
+// p ← p·decay + alpha·O over `total` elements (fp32 p, bf16 O; each product and
+// the sum rounded on their own).
+template <bool kVec>
+__global__ __launch_bounds__(kNormThreads) void muon_param_update_kernel(
+    float *__restrict__ p, const uint16_t *__restrict__ o, int64_t total, float decay,
+    float alpha) {
+#pragma clang fp contract(off)
+    const int64_t stride = int64_t(gridDim.x) * kNormThreads * 8;
+    for (int64_t e = (int64_t(blockIdx.x) * kNormThreads + threadIdx.x) * 8; e < total;
+         e += stride) {
+        if (kVec) {
+            const u32x4 ov = *reinterpret_cast<const u32x4 *>(o + e);
+            f32x4 p0 = *reinterpret_cast<const f32x4 *>(p + e);
+            f32x4 p1 = *reinterpret_cast<const f32x4 *>(p + e + 4);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                p0[2 * i] = p0[2 * i] * decay + alpha * bf16_bits_to_f32(ov[i] & 0xffffu);
+                p0[2 * i + 1] = p0[2 * i + 1] * decay + alpha * bf16_bits_to_f32(ov[i] >> 16);
+                p1[2 * i] = p1[2 * i] * decay + alpha * bf16_bits_to_f32(ov[i + 2] & 0xffffu);
+                p1[2 * i + 1] = p1[2 * i + 1] * decay + alpha * bf16_bits_to_f32(ov[i + 2] >> 16);
+            }
+            *reinterpret_cast<f32x4 *>(p + e) = p0;
+            *reinterpret_cast<f32x4 *>(p + e + 4) = p1;
+        } else {
+            const int64_t end = e + 8 < total ? e + 8 : total;
+            for (int64_t i = e; i < end; ++i) p[i] = p[i] * decay + alpha * bf16_bits_to_f32(o[i]);
+        }
+    }
+}
+
 }  // namespace
 
 int64_t norm_chunks(int64_t mn) { return (mn + kNormChunk - 1) / kNormChunk; }
+
+hipError_t launch_norm_scale(const uint16_t *x, uint16_t *y, const float *partial,
+                             int64_t batch, int64_t mn, bool vec, hipStream_t stream) {
+    const int64_t chunks = norm_chunks(mn);
+    const int64_t grid = batch * chunks;
+    if (grid <= 0 || grid >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+    int ch = static_cast<int>(chunks), v = vec ? 1 : 0;
+    void *a2[] = {&x, &y, &partial, &mn, &ch, &v};
+    return hipLaunchKernel(reinterpret_cast<const void *>(&norm_scale_kernel),
+                           dim3(static_cast<unsigned>(grid)), dim3(kNormThreads), a2, 0, stream);
+}
+
+hipError_t launch_muon_momentum(const float *g, float *buf, uint16_t *x0, float *partial,
+                                int64_t batch, int64_t mn, float w, float beta, bool nesterov,
+                                bool vec, hipStream_t stream) {
+    const int64_t chunks = norm_chunks(mn);
+    const int64_t grid = batch * chunks;
+    if (grid <= 0 || grid >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+    int ch = static_cast<int>(chunks), nv = nesterov ? 1 : 0;
+    void *args[] = {&g, &buf, &x0, &partial, &mn, &ch, &w, &beta, &nv};
+    const bool order8 = mn % 8 == 0;
+    const void *fn = order8 ? (vec ? reinterpret_cast<const void *>(&muon_momentum_kernel<true, true>)
+                                   : reinterpret_cast<const void *>(&muon_momentum_kernel<true, false>))
+                            : reinterpret_cast<const void *>(&muon_momentum_kernel<false, false>);
+    return hipLaunchKernel(fn, dim3(static_cast<unsigned>(grid)), dim3(kNormThreads), args, 0,
+                           stream);
+}
+
+hipError_t launch_muon_param_update(float *p, const uint16_t *o, int64_t total, float decay,
+                                    float alpha, bool vec, hipStream_t stream) {
+    if (total <= 0) return hipErrorInvalidValue;
+    // 8 elements per thread; at most 8 waves' worth of blocks per CU on 256 CUs,
+    // a grid-stride loop beyond that
+    const int64_t blocks = (total + kNormThreads * 8 - 1) / (kNormThreads * 8);
+    const unsigned grid = static_cast<unsigned>(blocks < 4096 ? blocks : 4096);
+    void *args[] = {&p, &o, &total, &decay, &alpha};
+    const void *fn = vec ? reinterpret_cast<const void *>(&muon_param_update_kernel<true>)
+                         : reinterpret_cast<const void *>(&muon_param_update_kernel<false>);
+    return hipLaunchKernel(fn, dim3(grid), dim3(kNormThreads), args, 0, stream);
+}
 
 hipError_t launch_normalize(const uint16_t *x, uint16_t *y, float *partial, int64_t batch,
                             int64_t mn, bool vec, hipStream_t stream) {

@@ -32,11 +32,23 @@ What it restates (reference file:line):
 * ``sparse_sign_input`` / ``polar_step_fused_sparse`` — ``polar_step_fused`` on sparse ±1
   inputs whose sums are exact in fp32 in any order, so a kernel must match it bit for bit
   at full size whatever its K split (no reference counterpart: a test device).
+* ``lerp_f32`` / ``muon_momentum`` / ``muon_param_update`` / ``muon_update_fused`` — the
+  Muon optimizer update around the iteration, which the reference leaves to its caller
+  (README.md:130) and whose algorithm lives in a dependency absent from the reference
+  tree: nanochat's ``Muon.step`` (karpathy/nanochat ``nanochat/muon.py``; the reference
+  was extracted from SwanHubX/nanochat-ascend PR #15, commit ae3d3a6b, README.md:247;
+  no pinned copy is available here).  Restated from the published Muon step (momentum
+  ``buf.lerp_(g, 1 - β)``, Nesterov ``g.lerp_(buf, β)``, orthogonalisation, ``p.add_(O,
+  alpha=-lr·sqrt(max(1, rows/cols)))``) plus decoupled weight decay ``p·(1 − lr·wd)``, in
+  float32 with every operation rounded on its own (torch.lerp's two-branch form, ATen
+  Lerp.h), the iteration with the rounding points above.
 
-How each function is pinned (``tests/test_oracle.py``): SVD closed form (one step maps
-singular values σ -> aσ + bσ³ + cσ⁵, five steps compose), textbook special cases of each
-stage, brute-force loops on tiny inputs, bf16 rounding against torch's RNE conversion, and
-planted mistakes that must fail those checks.
+How each function is pinned (``tests/test_oracle.py``, ``tests/test_muon_oracle.py``): SVD
+closed form (one step maps singular values σ -> aσ + bσ³ + cσ⁵, five steps compose),
+textbook special cases of each stage, brute-force loops on tiny inputs, bf16 rounding
+against torch's RNE conversion, for the Muon update the closed forms of momentum under a
+constant gradient, weight decay alone and the update's singular values, torch.lerp within
+one ulp, and planted mistakes that must fail those checks.
 """
 
 from __future__ import annotations
@@ -311,3 +323,46 @@ def scalar_polynomial(sigma, coefficients) -> np.ndarray:
         s = a * s + b * s**3 + c * s**5
     return s
 
+
+
+# ----------------------------------------------------------------------------- Muon update
+def lerp_f32(start, end, w) -> np.ndarray:
+    """torch.lerp's two-branch form (ATen Lerp.h) in float32, each operation rounded on its
+    own: start + w·(end − start) for |w| < 0.5, else end − (end − start)·(1 − w)."""
+    start = np.asarray(start, dtype=np.float32)
+    end = np.asarray(end, dtype=np.float32)
+    w = np.float32(w)
+    if abs(w) < np.float32(0.5):
+        return start + w * (end - start)
+    return end - (end - start) * (np.float32(1.0) - w)
+
+
+def muon_momentum(grad, buf, momentum: float, nesterov: bool):
+    """nanochat Muon.step: ``buf.lerp_(g, 1 - momentum)``; the iteration's input is
+    ``g.lerp(buf, momentum)`` (Nesterov) or ``buf``.  Weights rounded to fp32 as
+    torch does with Python floats: (float)(1 − momentum), (float)momentum.
+    Returns (new buf, iteration input), float32."""
+    new_buf = lerp_f32(buf, grad, np.float32(1.0 - momentum))
+    u = lerp_f32(grad, new_buf, np.float32(momentum)) if nesterov else new_buf
+    return new_buf, u
+
+
+def muon_param_update(param, o, lr: float, weight_decay: float, lr_scale: float) -> np.ndarray:
+    """param·(float)(1 − lr·wd) + (float)(−lr·lr_scale)·O in float32, each operation
+    rounded on its own (``p.mul_(1 - lr*wd); p.add_(O, alpha=-lr*scale)``)."""
+    decay = np.float32(1.0 - lr * weight_decay)
+    alpha = np.float32(-lr * lr_scale)
+    return np.asarray(param, dtype=np.float32) * decay + alpha * np.asarray(o, dtype=np.float32)
+
+
+def muon_update_fused(param, grad, buf, momentum: float, nesterov: bool, coefficients, lr: float,
+                      weight_decay: float, lr_scale: float):
+    """One Muon update of float32 [..., M, N] arrays: momentum, bf16 input, normalisation
+    and steps with the kernels' rounding points (M > N through the wrapper's transpose,
+    which the right-Gram form equals), then the parameter update.
+    Returns (new param, new buf, O) as float32, float32, float64."""
+    new_buf, u = muon_momentum(grad, buf, momentum, nesterov)
+    x = normalize_reference_rounding(bf16_round(u).astype(np.float64))
+    for a, b, c in coefficients:
+        x = wrapper_step(x, a, b, c)
+    return muon_param_update(param, x, lr, weight_decay, lr_scale), new_buf, x

@@ -35,7 +35,7 @@ def test_public_surface():
     assert muon_ascend950.polar_step is mf.polar_step
     assert muon_ascend950.polar_express is mf.polar_express
     assert mf.__version__ == "0.1.1" == muon_ascend950.__version__
-    assert mf.__all__ == ["COEFFICIENTS", "polar_express", "polar_step"]
+    assert mf.__all__ == ["COEFFICIENTS", "Muon", "muon_update", "polar_express", "polar_step"]
     # the reference's five triples (tests/test_polar_step.py:13-19)
     assert mf.COEFFICIENTS == tuple(tuple(t) for t in O.COEFFICIENTS)
 
@@ -125,6 +125,82 @@ def test_express_entry_validates_before_launch():
     # x and y overlap: rejected before anything launches (pointers never dereferenced)
     assert lib.muon_polar_express(16, 32, 16, big, 1, 4, 8, coeffs, 1, 1, None) == capi.ERR_INVALID_ARGUMENT
     assert "overlap" in capi.last_error()
+
+
+def test_muon_update_fake_and_schema():
+    schema = str(torch.ops.muon_ascend950.muon_update.default._schema)
+    assert schema == ("muon_ascend950::muon_update(Tensor(a!) param, Tensor grad, "
+                      "Tensor(b!) momentum_buffer, float momentum, bool nesterov, "
+                      "float[] coefficients, float lr, float weight_decay, float lr_scale) -> ()")
+    with FakeTensorMode():
+        # wide, batched, tall with N % 8 == 0, tall otherwise (transposed route),
+        # several leading dimensions, non-contiguous
+        for shape in [(5, 9), (2, 5, 9), (40, 16), (40, 7), (4, 3, 16, 8)]:
+            p = torch.empty(shape, dtype=torch.float32, device="cuda")
+            mf.muon_update(p, torch.empty_like(p), torch.zeros_like(p), lr=0.02)
+        # non-contiguous param and buffer, bf16 grad
+        p = torch.empty(9, 5, dtype=torch.float32, device="cuda").mT
+        b = torch.zeros(9, 5, dtype=torch.float32, device="cuda").mT
+        mf.muon_update(p, torch.empty(5, 9, dtype=torch.bfloat16, device="cuda"), b, lr=0.02)
+
+
+def test_muon_update_rejects_bad_arguments():
+    with FakeTensorMode():
+        p = torch.empty(8, 16, dtype=torch.float32, device="cuda")
+        g, b = torch.empty_like(p), torch.zeros_like(p)
+        with pytest.raises(TypeError, match="float32"):
+            mf.muon_update(p.bfloat16(), g, b, lr=0.1)
+        with pytest.raises(TypeError, match="grad"):
+            mf.muon_update(p, g.half(), b, lr=0.1)
+        with pytest.raises(ValueError, match="ndim"):
+            mf.muon_update(p[0], g[0], b[0], lr=0.1)
+        with pytest.raises(ValueError, match="one shape"):
+            mf.muon_update(p, g[:4], b, lr=0.1)
+        with pytest.raises(ValueError, match="coefficient triples"):
+            mf.muon_update(p, g, b, lr=0.1, ns_steps=6)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        cpu = torch.zeros(8, 16)
+        mf.muon_update(cpu, cpu.clone(), cpu.clone(), lr=0.1)
+    w = torch.nn.Parameter(torch.zeros(8, 16))
+    for kwargs in ({"lr": -1.0}, {"momentum": 1.5}, {"weight_decay": -0.1}, {"ns_steps": 0},
+                   {"ns_steps": 6}):
+        with pytest.raises(ValueError):
+            mf.Muon([w], **kwargs)
+
+
+def test_muon_default_lr_scale():
+    from muon_fusion_ascend950_amd.optim import default_lr_scale
+
+    assert default_lr_scale(512, 2048) == 1.0
+    assert default_lr_scale(2048, 512) == 2.0
+    assert default_lr_scale(300, 300) == 1.0
+
+
+def test_muon_entry_validates_before_launch():
+    lib = capi.load()
+    coeffs = (ctypes.c_double * 3)(1.0, 2.0, 3.0)
+    info = capi.query(1, 4, 8)
+    assert info.muon_workspace_bytes >= info.express_workspace_bytes + 4 * 8 * 2
+    big = info.muon_workspace_bytes
+    # distinct, non-overlapping fake addresses; nothing is dereferenced before the checks
+    p, g, b, ws = 1 << 20, 2 << 20, 3 << 20, 4 << 20
+
+    def call(*, p=p, g=g, b=b, ws=ws, size=big, m=4, n=8, momentum=0.95, steps=1, cf=coeffs,
+             lr=0.1, wd=0.0, scale=1.0):
+        return lib.muon_polar_muon_update(p, g, b, ws, size, 1, m, n, momentum, 1, cf, steps, lr,
+                                          wd, scale, None)
+
+    assert call(p=None) == capi.ERR_INVALID_ARGUMENT
+    assert call(steps=-1) == capi.ERR_INVALID_ARGUMENT
+    assert call(cf=None) == capi.ERR_INVALID_ARGUMENT
+    assert call(momentum=1.5) == capi.ERR_INVALID_ARGUMENT
+    assert call(lr=float("nan")) == capi.ERR_INVALID_ARGUMENT
+    assert call(size=big - 1) == capi.ERR_WORKSPACE
+    assert call(g=p + 64) == capi.ERR_INVALID_ARGUMENT and "overlap" in capi.last_error()
+    assert call(ws=b + 16) == capi.ERR_INVALID_ARGUMENT and "overlap" in capi.last_error()
+    tall = capi.query(1, 20, 12).muon_workspace_bytes
+    assert call(m=20, n=12, size=tall) == capi.ERR_INVALID_ARGUMENT
+    assert "n % 8 == 0" in capi.last_error()
 
 
 def test_loader_is_idempotent():
