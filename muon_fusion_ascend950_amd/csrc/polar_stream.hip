@@ -365,13 +365,16 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             __builtin_amdgcn_sched_barrier(0);
             mfmas(fr0, fc0);
             __builtin_amdgcn_sched_barrier(0);
-            if (k + 1 < nkl) {
-                if (kStages == 3 && k + 2 < nkl)
-                    wait_vm_barrier<Geo::kLoads>();  // panel k+2 may stay in flight
-                else
-                    wait_vm_barrier<0>();
-                load_frags(next, 0, fr0, fc0);
-            }
+            // Unconditional, also on the last step (nothing is in flight then, and
+            // the fragments read from the stale slot are not used): a branch around
+            // these LDS reads makes the compiler's wait counts on the join below
+            // assume none were issued, and the slice-3 MFMAs would then wait for
+            // all of them.
+            if (kStages == 3 && k + 2 < nkl)
+                wait_vm_barrier<Geo::kLoads>();  // panel k+2 may stay in flight
+            else
+                wait_vm_barrier<0>();
+            load_frags(next, 0, fr0, fc0);
             __builtin_amdgcn_sched_barrier(0);
             const bool more = k + kStages < nkl;
             mfmas_with_dma(fr1, fc1, kbeg + k + kStages, slot, more,
