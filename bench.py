@@ -89,8 +89,7 @@ def stage_times(batch: int, m: int, n: int, launches: int, warmup: int = 3):
     launched in step order through the C ABI with polar_step's workspace (A and P in
     it, the same stream-K split as in the step), `launches` times, with HIP events on
     torch's current stream (the launch stream) between the stages; each stage's time is
-    the sum of its event intervals / launches.  A stage call given a workspace clears
-    its own arrival counters (a one-block fill kernel, inside its interval)."""
+    the sum of its event intervals / launches."""
     import torch
     from muon_fusion_ascend950_amd import capi
 

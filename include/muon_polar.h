@@ -25,9 +25,10 @@
  * workgroup, and the last contributor of a tile sums the fp32 partials in a
  * fixed order (results are the same on every run of one device type, and equal
  * the unsplit ones to fp32 rounding).  The arrival counters and partial tiles
- * live in the workspace after A and P; every entry point that gets a workspace
- * clears the counters it uses itself.  Calls that share one workspace must not
- * overlap (use one workspace per concurrent stream).
+ * live in the workspace after A and P.  Each counter word carries the token of
+ * the launch that wrote it, and words of other launches count as zero, so the
+ * workspace needs no clearing (any content, graph replays included).  Calls that
+ * share one workspace must not overlap (use one workspace per concurrent stream).
  *
  * All functions are asynchronous on the given HIP stream (launch only, no
  * synchronisation) unless MUON_POLAR_DEBUG_SYNC is set in the environment, in

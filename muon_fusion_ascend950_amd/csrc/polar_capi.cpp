@@ -13,6 +13,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -114,7 +115,7 @@ struct Plan {
     bool stream;
     int waves[3];  // waves per workgroup of the DMA-fed kernel of each stage
     // polar_step's stream-K splits (gram, poly, apply) and their workspace areas
-    // after A and P: arrival counters (counter_stride words per stage), then
+    // after A and P: arrival words (counter_stride 64-bit words per stage), then
     // the fp32 partial slots shared by the three stages.
     SkSplit sk[3];
     bool sk_any;
@@ -304,7 +305,7 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     }
     p.counters_offset = 2 * align256(p.gram_bytes);
     p.partials_offset =
-        p.counters_offset + align256(size_t(3) * p.counter_stride * sizeof(uint32_t));
+        p.counters_offset + align256(size_t(3) * p.counter_stride * sizeof(uint64_t));
     p.workspace_bytes = p.partials_offset + align256(partial_bytes);
     p.express_x_offset = p.workspace_bytes;
     p.express_norm_offset = p.express_x_offset + align256(size_t(batch) * m * n * 2u);
@@ -339,8 +340,12 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // the stage entry points have no workspace and run one tile per workgroup).
 struct SkArea {
     float *partials;
-    uint32_t *counters;  // this stage's counters
+    uint64_t *counters;  // this stage's arrival words
 };
+
+// Launch tokens of the stream-K arrival words: a fresh one per launch, so words
+// left by other launches (or never written) count as zero and need no clearing.
+std::atomic<uint32_t> g_launch_token{1};
 
 // Launch one stage: DMA-fed kernel when allowed, register-staged otherwise.
 hipError_t launch_stage(Stage s, int bm, int bn, int waves, bool stream_ok, bool vec,
@@ -357,6 +362,7 @@ hipError_t launch_stage(Stage s, int bm, int bn, int waves, bool stream_ok, bool
         g.sk_iters = sk->sk_iters;
         g.partials = area->partials;
         g.counters = area->counters;
+        g.token = g_launch_token.fetch_add(1, std::memory_order_relaxed);
     }
     g.per_xcd = (g.dp_tiles + 7) / 8;
     if (stream_ok) return muon_polar::launch_stream(s, bm, bn, waves, g, stream);
@@ -366,7 +372,7 @@ hipError_t launch_stage(Stage s, int bm, int bn, int waves, bool stream_ok, bool
 SkArea sk_area(const Plan &p, void *workspace, int stage) {
     char *ws = static_cast<char *>(workspace);
     return SkArea{reinterpret_cast<float *>(ws + p.partials_offset),
-                  reinterpret_cast<uint32_t *>(ws + p.counters_offset) + stage * p.counter_stride};
+                  reinterpret_cast<uint64_t *>(ws + p.counters_offset) + stage * p.counter_stride};
 }
 
 int check_workspace(const Plan &p, const void *workspace, size_t workspace_bytes) {
@@ -379,19 +385,16 @@ int check_workspace(const Plan &p, const void *workspace, size_t workspace_bytes
     return MUON_POLAR_OK;
 }
 
-// Stream-K area of one stage call: null without a workspace (no split);
-// otherwise the stage's counters are cleared first.
+// Stream-K area of one stage call: null without a workspace (no split).
 int stage_area(const Plan &p, void *workspace, size_t workspace_bytes, int stage, SkArea &area,
-               const SkArea *&out, hipStream_t stream) {
+               const SkArea *&out) {
     out = nullptr;
     if (workspace == nullptr) return MUON_POLAR_OK;
     const int st = check_workspace(p, workspace, workspace_bytes);
     if (st != MUON_POLAR_OK) return st;
     area = sk_area(p, workspace, stage);
     out = &area;
-    if (p.sk[stage].sk_units == 0) return MUON_POLAR_OK;
-    return finish_stage(muon_polar::launch_zero_words(area.counters, p.counter_stride, stream),
-                        stream, "counter reset");
+    return MUON_POLAR_OK;
 }
 
 int run_gram(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
@@ -562,15 +565,6 @@ int run_steps(const Plan &p, void *workspace, const uint16_t *cur, uint16_t *out
               hipStream_t stream) {
     if (steps == 0) return MUON_POLAR_OK;
     char *ws = static_cast<char *>(workspace);
-    if (p.sk_any) {
-        // The stage kernels leave every counter they use at zero, so one clear
-        // covers all steps.
-        const int st = finish_stage(
-            muon_polar::launch_zero_words(reinterpret_cast<uint32_t *>(ws + p.counters_offset),
-                                          3 * p.counter_stride, stream),
-            stream, "counter reset");
-        if (st != MUON_POLAR_OK) return st;
-    }
     void *gram = ws;
     void *poly = ws + align256(p.gram_bytes);
     const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
@@ -621,7 +615,7 @@ int muon_polar_gram(const void *x, void *gram, void *workspace, size_t workspace
     if (!aligned16(gram)) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram must be 16-byte aligned");
     SkArea area{};
     const SkArea *ap = nullptr;
-    st = stage_area(p, workspace, workspace_bytes, 0, area, ap, stream);
+    st = stage_area(p, workspace, workspace_bytes, 0, area, ap);
     if (st != MUON_POLAR_OK) return st;
     return run_gram(p, x, gram, batch, m, n, ap, stream);
 }
@@ -639,7 +633,7 @@ int muon_polar_poly(const void *gram, void *poly, void *workspace, size_t worksp
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram and poly must be 16-byte aligned");
     SkArea area{};
     const SkArea *ap = nullptr;
-    st = stage_area(p, workspace, workspace_bytes, 1, area, ap, stream);
+    st = stage_area(p, workspace, workspace_bytes, 1, area, ap);
     if (st != MUON_POLAR_OK) return st;
     return run_poly(p, gram, poly, batch, b, c, ap, stream);
 }
@@ -657,7 +651,7 @@ int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
     if (!aligned16(poly)) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "poly must be 16-byte aligned");
     SkArea area{};
     const SkArea *ap = nullptr;
-    st = stage_area(p, workspace, workspace_bytes, 2, area, ap, stream);
+    st = stage_area(p, workspace, workspace_bytes, 2, area, ap);
     if (st != MUON_POLAR_OK) return st;
     return run_apply(p, poly, x, y, batch, m, n, a, ap, stream);
 }
@@ -677,16 +671,6 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
     }
     void *gram = workspace;
     void *poly = static_cast<char *>(workspace) + align256(p.gram_bytes);
-    if (p.sk_any) {
-        // Arrival counters start at zero; a fill kernel (not a memset node) keeps
-        // the step capturable in a graph.
-        st = finish_stage(
-            muon_polar::launch_zero_words(
-                reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + p.counters_offset),
-                3 * p.counter_stride, stream),
-            stream, "counter reset");
-        if (st != MUON_POLAR_OK) return st;
-    }
     const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
                              sk_area(p, workspace, 2)};
     return run_step(p, x, y, gram, poly, areas, batch, a, b, c, stream);

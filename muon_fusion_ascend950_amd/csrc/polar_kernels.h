@@ -60,7 +60,12 @@ struct GemmArgs {
     int32_t sk_units;               // 0 or a multiple of 8
     int64_t sk_iters;
     float *partials;                // 2 * sk_units slots of BM * BN floats
-    uint32_t *counters;             // one arrival counter per stream-K tile, zero on entry
+    // One arrival word per stream-K tile: (token << 32) | count.  A word holding
+    // another launch's token counts as zero, so the words need no clearing; the
+    // last contributor leaves (token << 32) | 0, which a replay of the same
+    // launch (a captured graph keeps its token) reads as zero too.
+    uint64_t *counters;
+    uint32_t token;                 // this launch's token
 };
 
 bool tile_supported(Stage s, int bm, int bn);
@@ -82,8 +87,6 @@ int stream_waves(int bm, int bn, int requested);
 // Workgroups of the DMA-fed kernel for (s, bm, bn, waves) resident per CU (0 on error).
 int stream_blocks_per_cu(Stage s, int bm, int bn, int waves);
 
-// Sets n 32-bit words at p to zero (stream-ordered, no memset node).
-hipError_t launch_zero_words(uint32_t *p, int64_t n, hipStream_t stream);
 
 // Per-matrix normalisation y = x / (‖x‖_F·1.01 + 1e-6) of `batch` matrices of mn
 // elements (reference recipe rounding points; polar_norm.hip).  `partial` holds

@@ -393,7 +393,11 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             // results do not depend on arrival order) and runs the epilogue.
             const int u0 = sk_unit_of(g, tstart), u1 = sk_unit_of(g, tstart + nk - 1);
             const uint32_t others = static_cast<uint32_t>(u1 - u0);
-            uint32_t *cnt = g.counters + lt;
+            uint64_t *cnt = g.counters + lt;
+            const uint64_t tok = uint64_t(g.token) << 32;
+            auto count_of = [&](uint64_t w) -> uint32_t {
+                return (w & 0xffffffff00000000ull) == tok ? static_cast<uint32_t>(w) : 0u;
+            };
             // Partials and counters are accessed device-coherently (sc1 stores and
             // loads, agent-scope atomics), so no whole-cache write-back or
             // invalidate is needed: a contributor's stores are complete before its
@@ -425,7 +429,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             };
             if (tid == 0)
-                s_arrived = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_arrived = count_of(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
             __syncthreads();
             bool last = __builtin_amdgcn_readfirstlane(s_arrived) == others;
             bool stored = false;
@@ -433,16 +437,26 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                 store_own();
                 stored = true;
                 __syncthreads();
-                if (tid == 0)
-                    s_arrived =
-                        __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (tid == 0) {
+                    // count this unit in: compare-and-swap, starting from zero when the
+                    // word holds another launch's token (each failed exchange means
+                    // another contributor got in, so at most two retries)
+                    uint64_t old = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    uint32_t before = count_of(old);
+                    while (!__hip_atomic_compare_exchange_strong(
+                        cnt, &old, tok | (before + 1u), __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT))
+                        before = count_of(old);
+                    s_arrived = before;
+                }
                 __syncthreads();
                 last = __builtin_amdgcn_readfirstlane(s_arrived) == others;
             }
             if (!last) continue;
-            // Every other contributor has counted itself in: the counter is this
-            // unit's alone now.  Leave it at zero for the next launch that uses it.
-            if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // Every other contributor has counted itself in: the word is this
+            // unit's alone now.  Leave a zero count under this launch's token (a
+            // replay of the launch reuses the token).
+            if (tid == 0) __hip_atomic_store(cnt, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             // Own partial first or second in the order: add the others to it in
             // place (x + y == y + x).  Further back: start from p(u1) in memory.
             const bool from_memory = u1 - unit >= 2;
@@ -571,10 +585,6 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     }
 }
 
-__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *p, int64_t n) {
-    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) p[i] = 0u;
-}
-
 template <int BM, int BN, Stage S>
 hipError_t launch_stream_one(const GemmArgs &g, int grid, int waves, hipStream_t stream) {
     GemmArgs copy = g;
@@ -673,15 +683,6 @@ int stream_blocks_per_cu(Stage s, int bm, int bn, int waves) {
             return occupancy_by_tile<Stage::ApplyR>(bm, bn, waves);
     }
     return 0;
-}
-
-hipError_t launch_zero_words(uint32_t *p, int64_t n, hipStream_t stream) {
-    if (n <= 0) return hipSuccess;
-    const int64_t blocks = (n + 255) / 256;
-    const int grid = static_cast<int>(blocks < 1024 ? blocks : 1024);
-    void *args[] = {&p, &n};
-    return hipLaunchKernel(reinterpret_cast<const void *>(&zero_words_kernel), dim3(grid), dim3(256),
-                           args, 0, stream);
 }
 
 }  // namespace muon_polar

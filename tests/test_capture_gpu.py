@@ -1,9 +1,12 @@
 """HIP-graph capture of polar_step, the op's registration checks, and gram invariants
 (GPU; marked ``gpu``).
 
-* A captured step (counter reset, three stage kernels, workspace from the graph's pool)
-  replays bit-identically to eager calls, replay after replay, with eager work on the same
-  buffers in between (the reference never tested capture).
+* A captured step (three stage kernels, workspace from the graph's pool) replays
+  bit-identically to eager calls, replay after replay, with eager work on the same buffers
+  in between (the reference never tested capture).  The stream-K arrival
+  words carry a launch token: a replay reuses its captured token and finds the zero counts
+  its last run left, eager launches on the same workspace in between use other tokens.
+* A workspace full of garbage gives the same bits as a fresh one (no clearing needed).
 * ``torch.library.opcheck``: schema and FakeTensor registration of the op
   (reference ``_loader.py:41-48``, ``binding.cpp:679``).
 * Gram invariants that pin stage 1 without a reference run: ``trace(A) = ‖X‖_F²`` and
@@ -40,8 +43,8 @@ def polar_step(x, a, b, c):
 
 @pytest.mark.parametrize("shape", [(8, 512, 2048), (2, 1024, 4096), (2, 150, 2050)])
 def test_graph_replays_match_eager(shape):
-    """(2, 1024, 4096) splits its gram stage (counter reset in the graph); (2, 150, 2050)
-    runs the register-staged kernels."""
+    """(2, 1024, 4096) splits its gram stage (stream-K arrival words in the graph's
+    workspace); (2, 150, 2050) runs the register-staged kernels."""
     x_static = O.make_input(shape, seed=30).to(DEV)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -60,6 +63,48 @@ def test_graph_replays_match_eager(shape):
         want = polar_step(x_new, *C0)  # eager, between replays
         torch.cuda.synchronize()
         assert torch.equal(y_static, want), f"replay {r} differs from eager"
+
+
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (2, 1024, 4096), (8, 512, 2048)])
+def test_garbage_workspace_and_shared_workspace_replays(shape):
+    """The C ABI step on a workspace filled with random bytes equals the step on a zeroed
+    one, bit for bit; a graph that captured a step on one workspace still replays
+    correctly after eager steps of other inputs ran on that same workspace."""
+    from muon_fusion_ascend950_amd import capi
+
+    batch, m, n = shape
+    print(f"garbage workspace {shape}", flush=True)
+    x = O.make_input(shape, seed=34).to(DEV)
+    ws, info = capi.alloc_workspace(batch, m, n)
+    gen = torch.Generator(device=DEV).manual_seed(35)
+    ws.copy_(torch.randint(0, 256, ws.shape, dtype=torch.uint8, device=DEV, generator=gen))
+    y_garbage = torch.empty_like(x)
+    capi.step(x, y_garbage, ws, *C0)
+    ws_zero = torch.zeros_like(ws)
+    y_zero = torch.empty_like(x)
+    capi.step(x, y_zero, ws_zero, *C0)
+    torch.cuda.synchronize()
+    assert torch.equal(y_garbage, y_zero)
+
+    y_graph = torch.empty_like(x)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        capi.step(x, y_graph, ws, *C0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        capi.step(x, y_graph, ws, *C0)
+    other = O.make_input(shape, seed=36).to(DEV)
+    y_other = torch.empty_like(x)
+    for r in range(3):
+        y_graph.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, y_zero), f"replay {r}"
+        capi.step(other, y_other, ws, *C0)  # eager, same workspace, another token
+        torch.cuda.synchronize()
 
 
 def test_opcheck_schema_and_fake():
