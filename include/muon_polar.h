@@ -30,6 +30,11 @@
  * workspace needs no clearing (any content, graph replays included).  Calls that
  * share one workspace must not overlap (use one workspace per concurrent stream).
  *
+ * Rows of n % 8 != 0 elements (m <= n): each step first copies X into a
+ * zero-padded [batch, m, roundup(n, 8)] buffer at the end of the workspace, so
+ * that the DMA-fed kernels (16-byte global->LDS transfers) serve every width; Y
+ * is written at its own width with 2-byte stores.
+ *
  * All functions are asynchronous on the given HIP stream (launch only, no
  * synchronisation) unless MUON_POLAR_DEBUG_SYNC is set in the environment, in
  * which case every stage synchronises the stream and reports kernel faults.
@@ -91,8 +96,9 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
 /* The three stages one at a time.  `workspace` is NULL (workspace_bytes
  * ignored: the stage runs one output tile per workgroup) or a buffer of
  * info.workspace_bytes, the same one muon_polar_step takes (gram / poly may be
- * its A / P areas), which lets the stage use the stream-K split exactly as
- * inside muon_polar_step.  The reference's stage launchers likewise take a
+ * its A / P areas), which lets the stage use the stream-K split (and, for
+ * n % 8 != 0, the padded copy of X) exactly as inside muon_polar_step, so the
+ * three calls reproduce the step bit for bit.  The reference's stage launchers likewise take a
  * device-side buffer (their tiling struct).  The stages take m <= n only. */
 
 /* Stage 1: gram[bt] = X[bt]·X[bt]ᵀ into a [batch, padded_rows, padded_rows]

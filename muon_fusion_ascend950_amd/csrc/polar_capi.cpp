@@ -57,10 +57,12 @@ struct Knobs {
     uint32_t stream;    // 1: DMA-fed kernels where eligible; 0: register-staged kernels only
     uint32_t stream_k;  // 1: stream-K split of a partial last round (polar_step only); 0: off
     uint32_t waves;     // waves per workgroup of the 256x256 DMA-fed kernels (4 or 8)
+    uint32_t depth[3];  // LDS ring slots of each stage's DMA-fed kernel (0: by shape)
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
                apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k &&
-               waves == o.waves;
+               waves == o.waves && depth[0] == o.depth[0] && depth[1] == o.depth[1] &&
+               depth[2] == o.depth[2];
     }
 };
 
@@ -90,6 +92,7 @@ struct PlanKeyHash {
         mix(k.knobs.stream);
         mix(k.knobs.stream_k);
         mix(k.knobs.waves);
+        mix(uint64_t(k.knobs.depth[0]) << 16 | uint64_t(k.knobs.depth[1]) << 8 | k.knobs.depth[2]);
         return static_cast<size_t>(h);
     }
 };
@@ -114,6 +117,7 @@ struct Plan {
     size_t gram_bytes, workspace_bytes;
     bool stream;
     int waves[3];  // waves per workgroup of the DMA-fed kernel of each stage
+    int depth[3];  // LDS ring slots of the DMA-fed kernel of each stage
     // polar_step's stream-K splits (gram, poly, apply) and their workspace areas
     // after A and P: arrival words (counter_stride 64-bit words per stage), then
     // the fp32 partial slots shared by the three stages.
@@ -121,6 +125,12 @@ struct Plan {
     bool sk_any;
     int64_t counter_stride;
     size_t counters_offset, partials_offset;
+    // Rows of n % 8 != 0 elements (m <= n): each step first copies X into a
+    // zero-padded [batch, m, np] buffer (np = roundup(n, 8)) at pad_offset, which
+    // the DMA-fed kernels read; Y is stored with 2-byte stores.
+    bool pad;
+    int64_t np;
+    size_t pad_offset;
     // muon_polar_express: one [batch, m, n] bf16 buffer, then the normalisation
     // partial sums, after the step's workspace
     size_t express_x_offset, express_norm_offset, express_workspace_bytes;
@@ -156,6 +166,13 @@ uint32_t default_apply_tile(int64_t m) {
     return 64;
 }
 
+// LDS ring depth by shape: two slots unless set otherwise (measured defaults
+// follow once swept).
+int default_depth(int bm, int bn, int waves, int64_t batch, int64_t tiles, int64_t k_steps) {
+    (void)bm, (void)bn, (void)waves, (void)batch, (void)tiles, (void)k_steps;
+    return 2;
+}
+
 int read_knobs(int64_t m, int64_t n, Knobs &k) {
     (void)n;
     k.gram_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_TILE", default_gram_tile(m)));
@@ -172,6 +189,11 @@ int read_knobs(int64_t m, int64_t n, Knobs &k) {
     k.waves = static_cast<uint32_t>(env_u64("MUON_POLAR_WAVES", kDefaultWaves));
     if (k.waves != 4 && k.waves != 8)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_WAVES must be 4 or 8");
+    k.depth[0] = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_DEPTH", 0));
+    k.depth[1] = static_cast<uint32_t>(env_u64("MUON_POLAR_POLY_DEPTH", 0));
+    k.depth[2] = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_DEPTH", 0));
+    for (uint32_t d : k.depth)
+        if (d > 8) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_*_DEPTH must be 0 (auto) or 2..8");
     if (!muon_polar::tile_supported(Stage::Gram, k.gram_tile, k.gram_tile))
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE must be 64, 128, 192 or 256");
     if (!muon_polar::tile_supported(Stage::Poly, k.poly_tile, k.poly_tile))
@@ -274,7 +296,9 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     // Stream-K needs the DMA-fed kernels (X rows of whole 16-byte chunks) and a
     // device to size the split for.
     int cus = 0;
-    const bool sk_ok = p.stream && knobs.stream_k != 0 && n % 8 == 0 && device >= 0 &&
+    p.pad = p.stream && !tall && n % 8 != 0;
+    p.np = p.pad ? round_up(n, 8) : n;
+    const bool sk_ok = p.stream && knobs.stream_k != 0 && (n % 8 == 0 || p.pad) && device >= 0 &&
                        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) ==
                            hipSuccess &&
                        cus > 0;
@@ -288,11 +312,23 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.sk_any = false;
     p.counter_stride = 0;
     size_t partial_bytes = 0;
-    for (int s = 0; s < 3; ++s)
+    for (int s = 0; s < 3; ++s) {
         p.waves[s] = muon_polar::stream_waves(tiles_bm[s], tiles_bn[s], static_cast<int>(knobs.waves));
+        p.depth[s] = knobs.depth[s] != 0
+                         ? static_cast<int>(knobs.depth[s])
+                         : default_depth(tiles_bm[s], tiles_bn[s], p.waves[s], batch, grids[s],
+                                         ksteps[s]);
+        if (p.stream && !muon_polar::stream_depth_supported(stages[s], tiles_bm[s], tiles_bn[s],
+                                                            p.waves[s], p.depth[s]))
+            return fail(MUON_POLAR_ERR_CONFIG,
+                        "no DMA-fed kernel for this tile, wave count and MUON_POLAR_*_DEPTH "
+                        "(128x128: 2 or 4; 64x64: 2, 4 or 8; 128x256 / 256x128: 2 or 3; "
+                        "others: 2)");
+    }
     for (int s = 0; s < 3; ++s) {
         const int occ = sk_ok ? muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s],
-                                                                 tiles_bn[s], p.waves[s])
+                                                                 tiles_bn[s], p.waves[s],
+                                                                 p.depth[s])
                               : 0;
         p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ,
                             sk_min_share(tiles_bm[s], tiles_bn[s]));
@@ -306,7 +342,9 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.counters_offset = 2 * align256(p.gram_bytes);
     p.partials_offset =
         p.counters_offset + align256(size_t(3) * p.counter_stride * sizeof(uint64_t));
-    p.workspace_bytes = p.partials_offset + align256(partial_bytes);
+    p.pad_offset = p.partials_offset + align256(partial_bytes);
+    p.workspace_bytes =
+        p.pad_offset + (p.pad ? align256(static_cast<size_t>(batch) * m * p.np * 2u) : 0u);
     p.express_x_offset = p.workspace_bytes;
     p.express_norm_offset = p.express_x_offset + align256(size_t(batch) * m * n * 2u);
     p.express_workspace_bytes =
@@ -348,7 +386,7 @@ struct SkArea {
 std::atomic<uint32_t> g_launch_token{1};
 
 // Launch one stage: DMA-fed kernel when allowed, register-staged otherwise.
-hipError_t launch_stage(Stage s, int bm, int bn, int waves, bool stream_ok, bool vec,
+hipError_t launch_stage(Stage s, int bm, int bn, int waves, int depth, bool stream_ok, bool vec,
                         GemmArgs &g, int64_t batch, int64_t grid, const SkSplit *sk,
                         const SkArea *area, hipStream_t stream) {
     g.total_tiles = static_cast<int32_t>(batch * g.tiles_per_batch);
@@ -365,7 +403,7 @@ hipError_t launch_stage(Stage s, int bm, int bn, int waves, bool stream_ok, bool
         g.token = g_launch_token.fetch_add(1, std::memory_order_relaxed);
     }
     g.per_xcd = (g.dp_tiles + 7) / 8;
-    if (stream_ok) return muon_polar::launch_stream(s, bm, bn, waves, g, stream);
+    if (stream_ok) return muon_polar::launch_stream(s, bm, bn, waves, depth, g, stream);
     return muon_polar::launch_gemm(s, bm, bn, vec, g, static_cast<int>(grid), stream);
 }
 
@@ -397,14 +435,15 @@ int stage_area(const Plan &p, void *workspace, size_t workspace_bytes, int stage
     return MUON_POLAR_OK;
 }
 
-int run_gram(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
-             const SkArea *area, hipStream_t stream) {
+// x: [batch, m, n] rows `ldx` elements apart (n, or np for the padded copy).
+int run_gram(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t batch, int64_t m,
+             int64_t n, const SkArea *area, hipStream_t stream) {
     GemmArgs g{};
     g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(x);
     g.out = static_cast<uint16_t *>(gram);
-    g.sb_row = g.sb_col = g.sb_epi = m * n;
+    g.sb_row = g.sb_col = g.sb_epi = m * ldx;
     g.sb_out = p.mp * p.mp;
-    g.ld_row = g.ld_col = g.ld_epi = static_cast<int32_t>(n);
+    g.ld_row = g.ld_col = g.ld_epi = static_cast<int32_t>(ldx);
     g.ld_out = static_cast<int32_t>(p.mp);
     g.row_rows = g.col_rows = static_cast<int32_t>(m);
     g.row_k = g.col_k = static_cast<int32_t>(n);
@@ -414,9 +453,10 @@ int run_gram(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m,
     g.tiles_per_batch = p.gram_nt * (p.gram_nt + 1) / 2;
     g.s_epi = 0.0f;
     g.s_acc = 1.0f;
-    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
-    const bool vec = (n % 8 == 0) && aligned16(x);
-    return finish_stage(launch_stage(Stage::Gram, p.gram_tile, p.gram_tile, p.waves[0],
+    g.out_vec = 1;
+    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
+    const bool vec = (ldx % 8 == 0) && aligned16(x);
+    return finish_stage(launch_stage(Stage::Gram, p.gram_tile, p.gram_tile, p.waves[0], p.depth[0],
                                      p.stream && vec, vec,
                                      g, batch, p.gram_grid, &p.sk[0], area, stream),
                         stream, "gram");
@@ -437,23 +477,28 @@ int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double 
     g.tiles_per_batch = p.poly_nt * (p.poly_nt + 1) / 2;
     g.s_epi = static_cast<float>(b);
     g.s_acc = static_cast<float>(c);
+    g.out_vec = 1;
     g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(p.mp * p.mp * 2);
-    return finish_stage(launch_stage(Stage::Poly, p.poly_tile, p.poly_tile, p.waves[1], p.stream,
+    return finish_stage(launch_stage(Stage::Poly, p.poly_tile, p.poly_tile, p.waves[1], p.depth[1], p.stream,
                                      true, g,
                                      batch, p.poly_grid, &p.sk[1], area, stream),
                         stream, "poly");
 }
 
-int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t batch, int64_t m,
-              int64_t n, double a, const SkArea *area, hipStream_t stream) {
+// x: [batch, m, n] rows `ldx` elements apart (n, or np for the padded copy);
+// y: [batch, m, n] dense.
+int run_apply(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y, int64_t batch,
+              int64_t m, int64_t n, double a, const SkArea *area, hipStream_t stream) {
     GemmArgs g{};
     g.rowop = static_cast<const uint16_t *>(poly);
     g.colop = g.epi = static_cast<const uint16_t *>(x);
     g.out = static_cast<uint16_t *>(y);
     g.sb_row = p.mp * p.mp;
-    g.sb_col = g.sb_epi = g.sb_out = m * n;
+    g.sb_col = g.sb_epi = m * ldx;
+    g.sb_out = m * n;
     g.ld_row = static_cast<int32_t>(p.mp);
-    g.ld_col = g.ld_epi = g.ld_out = static_cast<int32_t>(n);
+    g.ld_col = g.ld_epi = static_cast<int32_t>(ldx);
+    g.ld_out = static_cast<int32_t>(n);
     g.row_rows = g.row_k = static_cast<int32_t>(p.mp);
     g.col_rows = static_cast<int32_t>(n);
     g.col_k = static_cast<int32_t>(m);
@@ -466,15 +511,19 @@ int run_apply(const Plan &p, const void *poly, const void *x, void *y, int64_t b
     g.s_epi = static_cast<float>(a);
     g.s_acc = 1.0f;
     g.bytes_row = static_cast<uint32_t>(p.mp * p.mp * 2);
-    g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
+    g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
+    g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : 0;
     // Column tiles per raster group: 8 for wide X (4096 x 14336: 56 column tiles),
     // 4 for narrower ones (n = 4096: 16 column tiles; 476 vs 498 us).
     const uint64_t group_default = p.apply_tn >= 32 ? 8 : 4;
     g.group_n = static_cast<int32_t>(
         std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", group_default)));
-    const bool vec = (n % 8 == 0) && aligned16(x) && aligned16(y);
-    return finish_stage(launch_stage(Stage::Apply, p.apply_bm, p.apply_bn, p.waves[2],
-                                     p.stream && vec, vec,
+    // DMA-fed kernel: X rows of whole 16-byte chunks (Y any alignment: 2-byte
+    // stores when out_vec is 0); register-staged kernel: vectors on both or neither.
+    const bool xvec = (ldx % 8 == 0) && aligned16(x);
+    const bool vec = xvec && g.out_vec;
+    return finish_stage(launch_stage(Stage::Apply, p.apply_bm, p.apply_bn, p.waves[2], p.depth[2],
+                                     p.stream && xvec, vec,
                                      g, batch, p.apply_grid, &p.sk[2], area, stream),
                         stream, "apply");
 }
@@ -498,8 +547,9 @@ int run_gram_t(const Plan &p, const void *x, void *gram, int64_t batch, int64_t 
     g.tiles_per_batch = p.gram_nt * (p.gram_nt + 1) / 2;
     g.s_epi = 0.0f;
     g.s_acc = 1.0f;
+    g.out_vec = 1;
     g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
-    return finish_stage(launch_stage(Stage::GramT, p.gram_tile, p.gram_tile, p.waves[0], true, true,
+    return finish_stage(launch_stage(Stage::GramT, p.gram_tile, p.gram_tile, p.waves[0], p.depth[0], true, true,
                                      g, batch, p.gram_grid, &p.sk[0], area, stream),
                         stream, "gram");
 }
@@ -529,10 +579,11 @@ int run_apply_r(const Plan &p, const void *poly, const void *x, void *y, int64_t
     g.s_acc = 1.0f;
     g.bytes_row = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
     g.bytes_col = static_cast<uint32_t>(p.mp * p.mp * 2);
+    g.out_vec = 1;
     const uint64_t group_default = p.apply_tn >= 32 ? 8 : 4;
     g.group_n = static_cast<int32_t>(
         std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", group_default)));
-    return finish_stage(launch_stage(Stage::ApplyR, p.apply_bm, p.apply_bn, p.waves[2], true, true,
+    return finish_stage(launch_stage(Stage::ApplyR, p.apply_bm, p.apply_bn, p.waves[2], p.depth[2], true, true,
                                      g, batch, p.apply_grid, &p.sk[2], area, stream),
                         stream, "apply");
 }
@@ -546,16 +597,41 @@ int check_tall(const Plan &p, const void *x, const void *y) {
     return MUON_POLAR_OK;
 }
 
-// One step given the workspace areas: left form (m <= n) or right-Gram form.
-int run_step(const Plan &p, const void *x, void *y, void *gram, void *poly, const SkArea *areas,
-             int64_t batch, double a, double b, double c, hipStream_t stream) {
-    int st = p.tall ? run_gram_t(p, x, gram, batch, p.m, p.n, &areas[0], stream)
-                    : run_gram(p, x, gram, batch, p.m, p.n, &areas[0], stream);
+// Rows of n % 8 != 0 elements: copy X into the workspace's zero-padded buffer
+// and point (xs, ldx) at it; otherwise leave them at X.
+int pad_input(const Plan &p, void *workspace, const void *x, int64_t batch, hipStream_t stream,
+              const void *&xs, int64_t &ldx) {
+    if (!p.pad) return MUON_POLAR_OK;
+    uint16_t *xp = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + p.pad_offset);
+    const int st = finish_stage(
+        muon_polar::launch_pad_rows(static_cast<const uint16_t *>(x), xp, batch * p.m, p.n, stream),
+        stream, "pad");
+    if (st != MUON_POLAR_OK) return st;
+    xs = xp;
+    ldx = p.np;
+    return MUON_POLAR_OK;
+}
+
+// One step given the workspace: left form (m <= n) or right-Gram form; rows of
+// n % 8 != 0 elements are first copied into the zero-padded buffer.
+int run_step(const Plan &p, const void *x, void *y, void *workspace, int64_t batch, double a,
+             double b, double c, hipStream_t stream) {
+    char *ws = static_cast<char *>(workspace);
+    void *gram = ws;
+    void *poly = ws + align256(p.gram_bytes);
+    const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
+                             sk_area(p, workspace, 2)};
+    const void *xs = x;
+    int64_t ldx = p.n;
+    int st = pad_input(p, workspace, x, batch, stream, xs, ldx);
+    if (st != MUON_POLAR_OK) return st;
+    st = p.tall ? run_gram_t(p, x, gram, batch, p.m, p.n, &areas[0], stream)
+                    : run_gram(p, xs, ldx, gram, batch, p.m, p.n, &areas[0], stream);
     if (st != MUON_POLAR_OK) return st;
     st = run_poly(p, gram, poly, batch, b, c, &areas[1], stream);
     if (st != MUON_POLAR_OK) return st;
     return p.tall ? run_apply_r(p, poly, x, y, batch, p.m, p.n, a, &areas[2], stream)
-                  : run_apply(p, poly, x, y, batch, p.m, p.n, a, &areas[2], stream);
+                  : run_apply(p, poly, xs, ldx, y, batch, p.m, p.n, a, &areas[2], stream);
 }
 
 // `steps` steps from `cur` (the normalised input, in the chain's first buffer),
@@ -564,14 +640,9 @@ int run_steps(const Plan &p, void *workspace, const uint16_t *cur, uint16_t *out
               uint16_t *scratch, int64_t batch, const double *coefficients, int64_t steps,
               hipStream_t stream) {
     if (steps == 0) return MUON_POLAR_OK;
-    char *ws = static_cast<char *>(workspace);
-    void *gram = ws;
-    void *poly = ws + align256(p.gram_bytes);
-    const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
-                             sk_area(p, workspace, 2)};
     for (int64_t i = 0; i < steps; ++i) {
         uint16_t *next = (steps - i - 1) % 2 == 0 ? out : scratch;
-        const int st = run_step(p, cur, next, gram, poly, areas, batch, coefficients[3 * i],
+        const int st = run_step(p, cur, next, workspace, batch, coefficients[3 * i],
                                 coefficients[3 * i + 1], coefficients[3 * i + 2], stream);
         if (st != MUON_POLAR_OK) return st;
         cur = next;
@@ -617,7 +688,14 @@ int muon_polar_gram(const void *x, void *gram, void *workspace, size_t workspace
     const SkArea *ap = nullptr;
     st = stage_area(p, workspace, workspace_bytes, 0, area, ap);
     if (st != MUON_POLAR_OK) return st;
-    return run_gram(p, x, gram, batch, m, n, ap, stream);
+    // with the step's workspace, the step's route (padded copy for n % 8 != 0)
+    const void *xs = x;
+    int64_t ldx = n;
+    if (ap != nullptr) {
+        st = pad_input(p, workspace, x, batch, stream, xs, ldx);
+        if (st != MUON_POLAR_OK) return st;
+    }
+    return run_gram(p, xs, ldx, gram, batch, m, n, ap, stream);
 }
 
 int muon_polar_poly(const void *gram, void *poly, void *workspace, size_t workspace_bytes,
@@ -653,7 +731,13 @@ int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
     const SkArea *ap = nullptr;
     st = stage_area(p, workspace, workspace_bytes, 2, area, ap);
     if (st != MUON_POLAR_OK) return st;
-    return run_apply(p, poly, x, y, batch, m, n, a, ap, stream);
+    const void *xs = x;
+    int64_t ldx = n;
+    if (ap != nullptr) {
+        st = pad_input(p, workspace, x, batch, stream, xs, ldx);
+        if (st != MUON_POLAR_OK) return st;
+    }
+    return run_apply(p, poly, xs, ldx, y, batch, m, n, a, ap, stream);
 }
 
 int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_bytes, int64_t batch,
@@ -669,11 +753,7 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
         st = check_tall(p, x, y);
         if (st != MUON_POLAR_OK) return st;
     }
-    void *gram = workspace;
-    void *poly = static_cast<char *>(workspace) + align256(p.gram_bytes);
-    const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
-                             sk_area(p, workspace, 2)};
-    return run_step(p, x, y, gram, poly, areas, batch, a, b, c, stream);
+    return run_step(p, x, y, workspace, batch, a, b, c, stream);
 }
 
 int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace_bytes,

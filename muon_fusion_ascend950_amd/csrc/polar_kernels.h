@@ -42,6 +42,8 @@ struct GemmArgs {
     int32_t col_rows, col_k;                 // gram/poly: rows x K of colop; apply: cols x K
     int32_t k_loop;                          // K extent iterated (multiple of 64)
     int32_t out_rows, out_cols;              // store extent (apply only)
+    int32_t out_vec;                         // 1: out rows take 16-byte stores; 0: 2-byte
+                                             // stores (rows of n % 8 != 0 elements)
     int32_t tiles_m, tiles_n, tiles_per_batch;
     float s_epi, s_acc;  // poly: b, c;  apply: a, 1
     // streaming kernels only
@@ -76,16 +78,21 @@ hipError_t launch_gemm(Stage s, int bm, int bn, bool vec, const GemmArgs &g, int
 
 // DMA-fed kernels: X chunks of 16 B must be entirely inside or outside the matrix
 // (n % 8 == 0, 16-byte aligned X).  Grid is g.sk_units + 8 * g.per_xcd; `waves`
-// per workgroup as returned by stream_waves.
-hipError_t launch_stream(Stage s, int bm, int bn, int waves, const GemmArgs &g,
+// per workgroup as returned by stream_waves; `depth` LDS ring slots (one K-step
+// each), a combination stream_depth_supported accepts.
+hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const GemmArgs &g,
                          hipStream_t stream);
+
+// Whether a DMA-fed kernel exists for (s, bm, bn, waves, depth).
+bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth);
 
 // Waves per workgroup the DMA-fed kernel of a bm x bn tile runs with, given the
 // requested count (8 is available for 256x256 tiles; 4 otherwise).
 int stream_waves(int bm, int bn, int requested);
 
-// Workgroups of the DMA-fed kernel for (s, bm, bn, waves) resident per CU (0 on error).
-int stream_blocks_per_cu(Stage s, int bm, int bn, int waves);
+// Workgroups of the DMA-fed kernel for (s, bm, bn, waves, depth) resident per CU
+// (0 on error).
+int stream_blocks_per_cu(Stage s, int bm, int bn, int waves, int depth);
 
 
 // Per-matrix normalisation y = x / (‖x‖_F·1.01 + 1e-6) of `batch` matrices of mn
@@ -106,6 +113,10 @@ hipError_t launch_norm_scale(const uint16_t *x, uint16_t *y, const float *partia
 hipError_t launch_muon_momentum(const float *g, float *buf, uint16_t *x0, float *partial,
                                 int64_t batch, int64_t mn, float w, float beta, bool nesterov,
                                 bool vec, hipStream_t stream);
+// Xp [rows, roundup(n, 8)] = X [rows, n] with zero columns n.. (16-byte aligned xp).
+hipError_t launch_pad_rows(const uint16_t *x, uint16_t *xp, int64_t rows, int64_t n,
+                           hipStream_t stream);
+
 // p ← p·decay + alpha·O over `total` elements; vec: total % 8 == 0, 16-byte aligned.
 hipError_t launch_muon_param_update(float *p, const uint16_t *o, int64_t total, float decay,
                                     float alpha, bool vec, hipStream_t stream);

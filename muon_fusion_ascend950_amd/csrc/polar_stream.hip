@@ -33,28 +33,49 @@ namespace {
 // NW waves per workgroup in a 2 x NW/2 grid over the tile: 4 (one wave per
 // SIMD, 128x128 wave tiles for a 256x256 tile) or 8 (two waves per SIMD, 128x64
 // wave tiles: 1.5x the fragment reads, but one wave's LDS and barrier waits are
-// covered by the other's MFMAs).
-template <int BM, int BN, int NW>
+// covered by the other's MFMAs).  D = ring depth (LDS slots of one K-step each):
+// panels k+1 .. k+D-1 are in flight while step k is multiplied.  Two slots suit
+// the MFMA-bound shapes (a third measured slower at 4096 x 14336: more DMA in
+// flight competes with the fragment reads); deeper rings serve latency-bound
+// launches with few K-steps per workgroup, where each step would otherwise wait
+// for one full memory round trip.
+template <int BM, int BN, int NW, int D>
 struct StreamGeom {
     static constexpr int kThreads = 64 * NW;
     static constexpr int kABytes = BM * kBK * 2;        // row-operand panel per K-step
     static constexpr int kBBytes = BN * kBK * 2;        // col-operand panel per K-step
     static constexpr int kStageBytes = kABytes + kBBytes;
-    // Ring depth.  A third slot (where it fits in LDS) measured slower on every
-    // tile shape: more DMA in flight competes with the fragment reads; the
-    // loop below is written for either depth.
-    static constexpr int kStages = 2;
+    static constexpr int kStages = D;
     static constexpr int kLoadsA = kABytes / 1024 / NW;  // DMA instructions per wave
     static constexpr int kLoadsB = kBBytes / 1024 / NW;
     static constexpr int kLoads = kLoadsA + kLoadsB;
     static constexpr int kTileBytes = BM * BN * 2;       // bf16 output tile (epilogue)
     static constexpr int kEpiLoads = kTileBytes / 1024 / NW;
+    // The epilogue operand tile fits one ring slot (BM, BN <= 128): it is fetched
+    // into the first slot the K loop stops refilling, so its latency overlaps the
+    // last K-steps instead of following them.
+    static constexpr bool kEpiInSlot = kTileBytes <= kStageBytes && D >= 3;
+    static_assert(D >= 2 && D <= 8, "ring depth");
+    static_assert((D - 1) * kLoads + kEpiLoads <= 63, "vmcnt range");
     static_assert(kLoadsA >= 1 && kLoadsB >= 1 && kABytes % (1024 * NW) == 0 &&
                       kBBytes % (1024 * NW) == 0,
                   "panels must split into whole 1 KiB DMA blocks per wave");
     static_assert(kTileBytes <= kStages * kStageBytes, "epilogue tile must fit the ring");
     static_assert(kTileBytes % (1024 * NW) == 0, "epilogue DMA is whole 1 KiB blocks per wave");
 };
+
+// s_waitcnt vmcnt(n * LOADS), workgroup barrier; n < NMAX known only at run time.
+template <int LOADS, int NMAX, int EXTRA = 0>
+__device__ __forceinline__ void wait_panels_barrier(int n) {
+    if constexpr (NMAX <= 1) {
+        wait_vm_barrier<EXTRA>();
+    } else {
+        if (n >= NMAX - 1)
+            wait_vm_barrier<(NMAX - 1) * LOADS + EXTRA>();
+        else
+            wait_panels_barrier<LOADS, NMAX - 1, EXTRA>(n);
+    }
+}
 
 // Epilogue tile in LDS: [BM][BN] bf16.  BN a power of two: 16-byte chunk c of
 // row r is stored at chunk position c ^ ((r ^ (r >> 5)) & (BN/8 - 1)), so 32
@@ -90,9 +111,9 @@ __device__ __forceinline__ int sk_slot(const GemmArgs &g, int u, int st) {
     return 2 * u + (st != static_cast<int>(sk_bound(g, u) / g.k_steps));
 }
 
-template <int BM, int BN, Stage S, int NW>
+template <int BM, int BN, Stage S, int NW, int D>
 __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
-    using Geo = StreamGeom<BM, BN, NW>;
+    using Geo = StreamGeom<BM, BN, NW, D>;
     constexpr int kThreads = Geo::kThreads;
     constexpr int WM = BM / 2, WN = BN / (NW / 2);
     constexpr int SM = WM / 32, SN = WN / 32;
@@ -273,6 +294,30 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             for (int d = 0; d < Geo::kLoads; ++d) dma_one(d, step, slot, tail);
         };
 
+        // Epilogue operand tile (A for poly, X for apply) -> LDS ring slot `eslot`
+        // (the tile may span several slots from slot 0), rows/cols outside the
+        // matrix read as zero.
+        auto issue_epi = [&](int eslot) {
+            if constexpr (Tr::kEpiOperand) {
+                const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
+                constexpr int kChunksPerRow = BN / 8;
+#pragma unroll
+                for (int d = 0; d < Geo::kEpiLoads; ++d) {
+                    // LDS chunk q of the tile (row q / kChunksPerRow, position q %
+                    // kChunksPerRow) receives global chunk epi_pos(row, position).
+                    const int blk = wave * Geo::kEpiLoads + d;
+                    const int q = blk * 64 + lane;
+                    const int row = q / kChunksPerRow;
+                    const int c = epi_pos<BN>(row, q - row * kChunksPerRow);
+                    const int gr = row0 + row, gc = col0 + 8 * c;
+                    const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
+                                           ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
+                                           : kOob;
+                    dma_16B(rs_epi, smem_base + eslot * Geo::kStageBytes + blk * 1024, v);
+                }
+            }
+        };
+
         // -------------------------------------------------------- main loop
         f32x16 acc[SM][SN];
 #pragma unroll
@@ -331,23 +376,26 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         //   wait panel k+1, barrier | frags(next s0) | mfma(s3) + DMA panel k+kStages -> slot
         // The barrier sits where every wave has read all of step k's slot into
         // registers; panels k+2 .. k+kStages-1 may still be in flight there.
+        // With the epilogue tile in a slot (kEpiInSlot), the first step that issues
+        // no panel (k = nkl - kStages) issues the epilogue operand tile into its
+        // slot instead; every later wait lets those loads stay in flight.
         const int nkl = kend - kbeg;
+        constexpr bool kEpiPrefetch = Tr::kEpiOperand && Geo::kEpiInSlot;
         bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
-        issue_all(kbeg, 0);
-        if (nkl > 1) issue_all(kbeg + 1, 1);
-        if constexpr (kStages == 3) {
-            if (nkl > 2) issue_all(kbeg + 2, 2);
-            if (nkl > 2)
-                wait_vm_barrier<2 * Geo::kLoads>();
-            else if (nkl > 1)
-                wait_vm_barrier<Geo::kLoads>();
-            else
-                wait_vm_barrier<0>();
+        const int npro = nkl < kStages ? nkl : kStages;
+        for (int i = 0; i < npro; ++i) issue_all(kbeg + i, i);
+        int epi_slot = 0;
+        if constexpr (kEpiPrefetch) {
+            if (nkl < kStages) {
+                epi_slot = nkl;  // a slot the K loop never fills
+                issue_epi(epi_slot);
+                wait_panels_barrier<Geo::kLoads, kStages, Geo::kEpiLoads>(npro - 1);
+            } else {
+                epi_slot = (nkl - kStages) % kStages;
+                wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
+            }
         } else {
-            if (nkl > 1)
-                wait_vm_barrier<Geo::kLoads>();
-            else
-                wait_vm_barrier<0>();
+            wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
         }
         load_frags(0, 0, fr0, fc0);
         int slot = 0;
@@ -365,21 +413,26 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             __builtin_amdgcn_sched_barrier(0);
             mfmas(fr0, fc0);
             __builtin_amdgcn_sched_barrier(0);
-            // Unconditional, also on the last step (nothing is in flight then, and
-            // the fragments read from the stale slot are not used): a branch around
-            // these LDS reads makes the compiler's wait counts on the join below
-            // assume none were issued, and the slice-3 MFMAs would then wait for
-            // all of them.
-            if (kStages == 3 && k + 2 < nkl)
-                wait_vm_barrier<Geo::kLoads>();  // panel k+2 may stay in flight
+            // Wait for panel k+1; panels k+2 .. min(k+kStages-1, nkl-1) (and the
+            // epilogue tile once issued) may stay in flight.  Unconditional, also
+            // on the last step (nothing is in flight then, and the fragments read
+            // from the stale slot are not used): a branch around these LDS reads
+            // makes the compiler's wait counts on the join below assume none were
+            // issued, and the slice-3 MFMAs would then wait for all of them.
+            const int ahead = nkl - k - 2;
+            if (kEpiPrefetch && k > nkl - kStages)
+                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(ahead);
             else
-                wait_vm_barrier<0>();
+                wait_panels_barrier<Geo::kLoads, kStages - 1>(ahead);
             load_frags(next, 0, fr0, fc0);
             __builtin_amdgcn_sched_barrier(0);
             const bool more = k + kStages < nkl;
             mfmas_with_dma(fr1, fc1, kbeg + k + kStages, slot, more,
                            more && is_tail(kbeg + k + kStages));
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kEpiPrefetch) {
+                if (k == nkl - kStages) issue_epi(epi_slot);
+            }
             slot = next;
         }
         // All waves are done with the ring (and no DMA is outstanding).
@@ -493,29 +546,12 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         }
 
         // -------------------------------------------------------- epilogue
-        uint16_t *tile = smem;
+        uint16_t *tile = smem + epi_slot * (Geo::kStageBytes / 2);
         uint16_t *out = g.out + bt * g.sb_out;
         const bool diag = Tr::kSymmetric && (tm == tn);
 
-        if constexpr (Tr::kEpiOperand) {
-            // Epilogue operand tile (A for poly, X for apply) -> LDS, rows/cols outside
-            // the matrix read as zero.
-            const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
-            constexpr int kChunksPerRow = BN / 8;
-#pragma unroll
-            for (int d = 0; d < Geo::kEpiLoads; ++d) {
-                // LDS chunk q of the tile (row q / kChunksPerRow, position q %
-                // kChunksPerRow) receives global chunk epi_pos(row, position).
-                const int blk = wave * Geo::kEpiLoads + d;
-                const int q = blk * 64 + lane;
-                const int row = q / kChunksPerRow;
-                const int c = epi_pos<BN>(row, q - row * kChunksPerRow);
-                const int gr = row0 + row, gc = col0 + 8 * c;
-                const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
-                                       ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
-                                       : kOob;
-                dma_16B(rs_epi, smem_base + blk * 1024, v);
-            }
+        if constexpr (Tr::kEpiOperand && !kEpiPrefetch) {
+            issue_epi(0);
             wait_vm_barrier<0>();
         }
 
@@ -563,7 +599,15 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                 v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
                           hh[6] | (hh[7] << 16)};
             }
-            *reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc) = v;
+            if (Tr::kSymmetric || g.out_vec) {
+                *reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc) = v;
+            } else {
+                // rows of n % 8 != 0 elements: 2-byte stores up to the last column
+                uint16_t *dst = out + gr * g.ld_out + gc;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (gc + e < g.out_cols) dst[e] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
+            }
         }
 
         // Mirrored store (symmetric stages, off-diagonal tiles): row c of the
@@ -585,64 +629,73 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     }
 }
 
+// Instantiated (tile, waves, depth) combinations: 256x256 with 8 or 4 waves and
+// two slots; smaller tiles with 4 waves and the depths their LDS allows
+// (128x128: 2 or 4 slots of 32 KiB; 64x64: 2, 4 or 8 of 16 KiB; 128x256 and
+// 256x128: 2 or 3 of 48 KiB; 192x192: 2).
+template <int BM, int BN>
+constexpr bool depth_ok(int waves, int depth) {
+    if (BM == 256 && BN == 256) return depth == 2 && (waves == 8 || waves == 4);
+    if (waves != 4) return false;
+    if (BM == 128 && BN == 128) return depth == 2 || depth == 4;
+    if (BM == 64 && BN == 64) return depth == 2 || depth == 4 || depth == 8;
+    if (BM != BN) return depth == 2 || depth == 3;
+    return depth == 2;
+}
+
+template <int BM, int BN, Stage S, int NW, int D>
+const void *kernel_ptr() {
+    return reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, NW, D>);
+}
+
+// Kernel of (BM, BN, S) for the given waves and depth, or null.
 template <int BM, int BN, Stage S>
-hipError_t launch_stream_one(const GemmArgs &g, int grid, int waves, hipStream_t stream) {
-    GemmArgs copy = g;
-    void *args[] = {&copy};
+const void *kernel_for(int waves, int depth) {
+    if (!depth_ok<BM, BN>(waves, depth)) return nullptr;
     if constexpr (BM == 256 && BN == 256) {
-        if (waves == 8)
-            return hipLaunchKernel(reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, 8>),
-                                   dim3(grid), dim3(512), args, 0, stream);
+        return waves == 8 ? kernel_ptr<BM, BN, S, 8, 2>() : kernel_ptr<BM, BN, S, 4, 2>();
+    } else if constexpr (BM == 128 && BN == 128) {
+        return depth == 4 ? kernel_ptr<BM, BN, S, 4, 4>() : kernel_ptr<BM, BN, S, 4, 2>();
+    } else if constexpr (BM == 64 && BN == 64) {
+        return depth == 8   ? kernel_ptr<BM, BN, S, 4, 8>()
+               : depth == 4 ? kernel_ptr<BM, BN, S, 4, 4>()
+                            : kernel_ptr<BM, BN, S, 4, 2>();
+    } else if constexpr (BM != BN) {
+        return depth == 3 ? kernel_ptr<BM, BN, S, 4, 3>() : kernel_ptr<BM, BN, S, 4, 2>();
+    } else {
+        return kernel_ptr<BM, BN, S, 4, 2>();
     }
-    if (waves != 4) return hipErrorInvalidValue;
-    return hipLaunchKernel(reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, 4>),
-                           dim3(grid), dim3(256), args, 0, stream);
 }
 
 template <Stage S>
-hipError_t launch_stream_by_tile(int bm, int bn, int waves, const GemmArgs &g, int grid,
-                                 hipStream_t stream) {
-    if (bm == 64 && bn == 64) return launch_stream_one<64, 64, S>(g, grid, waves, stream);
-    if (bm == 128 && bn == 128) return launch_stream_one<128, 128, S>(g, grid, waves, stream);
-    if (bm == 256 && bn == 256) return launch_stream_one<256, 256, S>(g, grid, waves, stream);
+const void *kernel_by_tile(int bm, int bn, int waves, int depth) {
+    if (bm == 64 && bn == 64) return kernel_for<64, 64, S>(waves, depth);
+    if (bm == 128 && bn == 128) return kernel_for<128, 128, S>(waves, depth);
+    if (bm == 256 && bn == 256) return kernel_for<256, 256, S>(waves, depth);
     if constexpr (S == Stage::Gram || S == Stage::Poly) {
-        if (bm == 192 && bn == 192) return launch_stream_one<192, 192, S>(g, grid, waves, stream);
+        if (bm == 192 && bn == 192) return kernel_for<192, 192, S>(waves, depth);
     }
     if constexpr (!StageTraits<S>::kSymmetric) {
-        if (bm == 128 && bn == 256) return launch_stream_one<128, 256, S>(g, grid, waves, stream);
-        if (bm == 256 && bn == 128) return launch_stream_one<256, 128, S>(g, grid, waves, stream);
+        if (bm == 128 && bn == 256) return kernel_for<128, 256, S>(waves, depth);
+        if (bm == 256 && bn == 128) return kernel_for<256, 128, S>(waves, depth);
     }
-    return hipErrorInvalidValue;
+    return nullptr;
 }
 
-template <int BM, int BN, Stage S>
-int occupancy_one(int waves) {
-    int n = 0;
-    hipError_t e = hipErrorInvalidValue;
-    if constexpr (BM == 256 && BN == 256) {
-        if (waves == 8)
-            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &n, reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, 8>), 512, 0);
+const void *stream_kernel(Stage s, int bm, int bn, int waves, int depth) {
+    switch (s) {
+        case Stage::Gram:
+            return kernel_by_tile<Stage::Gram>(bm, bn, waves, depth);
+        case Stage::Poly:
+            return kernel_by_tile<Stage::Poly>(bm, bn, waves, depth);
+        case Stage::Apply:
+            return kernel_by_tile<Stage::Apply>(bm, bn, waves, depth);
+        case Stage::GramT:
+            return kernel_by_tile<Stage::GramT>(bm, bn, waves, depth);
+        case Stage::ApplyR:
+            return kernel_by_tile<Stage::ApplyR>(bm, bn, waves, depth);
     }
-    if (waves == 4)
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, 4>), 256, 0);
-    return e == hipSuccess ? n : 0;
-}
-
-template <Stage S>
-int occupancy_by_tile(int bm, int bn, int waves) {
-    if (bm == 64 && bn == 64) return occupancy_one<64, 64, S>(waves);
-    if (bm == 128 && bn == 128) return occupancy_one<128, 128, S>(waves);
-    if (bm == 256 && bn == 256) return occupancy_one<256, 256, S>(waves);
-    if constexpr (S == Stage::Gram || S == Stage::Poly) {
-        if (bm == 192 && bn == 192) return occupancy_one<192, 192, S>(waves);
-    }
-    if constexpr (!StageTraits<S>::kSymmetric) {
-        if (bm == 128 && bn == 256) return occupancy_one<128, 256, S>(waves);
-        if (bm == 256 && bn == 128) return occupancy_one<256, 128, S>(waves);
-    }
-    return 0;
+    return nullptr;
 }
 
 }  // namespace
@@ -651,38 +704,26 @@ int stream_waves(int bm, int bn, int requested) {
     return (bm == 256 && bn == 256 && requested == 8) ? 8 : 4;
 }
 
-hipError_t launch_stream(Stage s, int bm, int bn, int waves, const GemmArgs &g,
-                         hipStream_t stream) {
-    const int grid = g.sk_units + 8 * g.per_xcd;
-    switch (s) {
-        case Stage::Gram:
-            return launch_stream_by_tile<Stage::Gram>(bm, bn, waves, g, grid, stream);
-        case Stage::Poly:
-            return launch_stream_by_tile<Stage::Poly>(bm, bn, waves, g, grid, stream);
-        case Stage::Apply:
-            return launch_stream_by_tile<Stage::Apply>(bm, bn, waves, g, grid, stream);
-        case Stage::GramT:
-            return launch_stream_by_tile<Stage::GramT>(bm, bn, waves, g, grid, stream);
-        case Stage::ApplyR:
-            return launch_stream_by_tile<Stage::ApplyR>(bm, bn, waves, g, grid, stream);
-    }
-    return hipErrorInvalidValue;
+bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth) {
+    return stream_kernel(s, bm, bn, waves, depth) != nullptr;
 }
 
-int stream_blocks_per_cu(Stage s, int bm, int bn, int waves) {
-    switch (s) {
-        case Stage::Gram:
-            return occupancy_by_tile<Stage::Gram>(bm, bn, waves);
-        case Stage::Poly:
-            return occupancy_by_tile<Stage::Poly>(bm, bn, waves);
-        case Stage::Apply:
-            return occupancy_by_tile<Stage::Apply>(bm, bn, waves);
-        case Stage::GramT:
-            return occupancy_by_tile<Stage::GramT>(bm, bn, waves);
-        case Stage::ApplyR:
-            return occupancy_by_tile<Stage::ApplyR>(bm, bn, waves);
-    }
-    return 0;
+hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const GemmArgs &g,
+                         hipStream_t stream) {
+    const void *k = stream_kernel(s, bm, bn, waves, depth);
+    if (k == nullptr) return hipErrorInvalidValue;
+    const int grid = g.sk_units + 8 * g.per_xcd;
+    GemmArgs copy = g;
+    void *args[] = {&copy};
+    return hipLaunchKernel(k, dim3(grid), dim3(64 * waves), args, 0, stream);
+}
+
+int stream_blocks_per_cu(Stage s, int bm, int bn, int waves, int depth) {
+    const void *k = stream_kernel(s, bm, bn, waves, depth);
+    if (k == nullptr) return 0;
+    int n = 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 64 * waves, 0) == hipSuccess ? n
+                                                                                             : 0;
 }
 
 }  // namespace muon_polar

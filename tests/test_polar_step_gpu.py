@@ -284,9 +284,10 @@ def assert_close_kernels(a: torch.Tensor, b: torch.Tensor):
 @pytest.mark.parametrize("shape", [(2, 150, 2050), (1, 129, 130), (3, 300, 701), (2, 100, 512)])
 def test_masking_equals_zero_padding(monkeypatch, shape):
     """Reference binding pads to 128/16 and crops (binding.cpp:630-672); masking must
-    give the same numbers: bit for bit within one kernel family, to bf16 precision
-    when the padded shape switches to the DMA-fed kernels.  (Unsplit kernels: a
-    stream-K split depends on the tile count, which padding changes.)"""
+    give the same numbers, bit for bit: rows of n % 8 != 0 elements reach the same
+    DMA-fed kernels through a zero-padded copy, and the register-staged family
+    (MUON_POLAR_STREAM=0) masks element-wise.  (Unsplit kernels: a stream-K split
+    depends on the tile count, which padding changes.)"""
     monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
     x = O.make_input(shape, seed=7).to(DEV)
     batch, m, n = shape
@@ -297,10 +298,7 @@ def test_masking_equals_zero_padding(monkeypatch, shape):
     y = polar_step(x, *C0)
     yp = polar_step(padded, *C0)[:, :m, :n]
     torch.cuda.synchronize()
-    if n % 8 == 0:  # same kernel family on both sides
-        assert torch.equal(y, yp)
-    else:
-        assert_close_kernels(y, yp)
+    assert torch.equal(y, yp)
     monkeypatch.setenv("MUON_POLAR_STREAM", "0")
     ys = polar_step(x, *C0)
     yps = polar_step(padded, *C0)[:, :m, :n]
