@@ -152,12 +152,12 @@ constexpr uint32_t kDefaultWaves = 8;
 
 uint32_t default_gram_tile(int64_t m) {
     if (m >= 3072) return 256;
-    if (m > 256) return 128;
+    if (m > 512) return 128;
     return 64;
 }
 uint32_t default_poly_tile(int64_t m) {
     if (m >= 4096) return 256;
-    if (m > 256) return 128;
+    if (m > 512) return 128;
     return 64;
 }
 uint32_t default_apply_tile(int64_t m) {
@@ -166,10 +166,13 @@ uint32_t default_apply_tile(int64_t m) {
     return 64;
 }
 
-// LDS ring depth by shape: two slots unless set otherwise (measured defaults
-// follow once swept).
-int default_depth(int bm, int bn, int waves, int64_t batch, int64_t tiles, int64_t k_steps) {
-    (void)bm, (void)bn, (void)waves, (void)batch, (void)tiles, (void)k_steps;
+// LDS ring depth by shape.  Four slots where they cost no parallelism: 64x64
+// tiles (two workgroups per CU still fit) and 128x128 tiles when every tile has
+// a CU of its own anyway (poly at [2, 2048, 8192]: 288 -> 270 us per step).
+// Otherwise two: deeper rings lower the occupancy of the MFMA-bound shapes.
+int default_depth(int bm, int bn, int64_t tiles, int cus) {
+    if (bm == 64 && bn == 64) return 4;
+    if (bm == 128 && bn == 128 && cus > 0 && tiles <= cus) return 4;
     return 2;
 }
 
@@ -296,12 +299,12 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     // Stream-K needs the DMA-fed kernels (X rows of whole 16-byte chunks) and a
     // device to size the split for.
     int cus = 0;
+    if (device < 0 ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+        cus = 0;
     p.pad = p.stream && !tall && n % 8 != 0;
     p.np = p.pad ? round_up(n, 8) : n;
-    const bool sk_ok = p.stream && knobs.stream_k != 0 && (n % 8 == 0 || p.pad) && device >= 0 &&
-                       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) ==
-                           hipSuccess &&
-                       cus > 0;
+    const bool sk_ok = p.stream && knobs.stream_k != 0 && (n % 8 == 0 || p.pad) && cus > 0;
     const int tiles_bm[3] = {p.gram_tile, p.poly_tile, p.apply_bm};
     const int tiles_bn[3] = {p.gram_tile, p.poly_tile, p.apply_bn};
     const Stage stages[3] = {tall ? Stage::GramT : Stage::Gram, Stage::Poly,
@@ -316,8 +319,7 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
         p.waves[s] = muon_polar::stream_waves(tiles_bm[s], tiles_bn[s], static_cast<int>(knobs.waves));
         p.depth[s] = knobs.depth[s] != 0
                          ? static_cast<int>(knobs.depth[s])
-                         : default_depth(tiles_bm[s], tiles_bn[s], p.waves[s], batch, grids[s],
-                                         ksteps[s]);
+                         : default_depth(tiles_bm[s], tiles_bn[s], grids[s], cus);
         if (p.stream && !muon_polar::stream_depth_supported(stages[s], tiles_bm[s], tiles_bn[s],
                                                             p.waves[s], p.depth[s]))
             return fail(MUON_POLAR_ERR_CONFIG,

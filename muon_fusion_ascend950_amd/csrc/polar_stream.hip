@@ -124,6 +124,12 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     static_assert(!Tr::kColNC || 512 % BN == 0, "N-contiguous panel rows must tile 1 KiB");
 
     constexpr int kStages = Geo::kStages;
+    // Apply stages: a·X is added into the accumulators at the K-steps whose operand
+    // panel holds this tile's own X values (apply: the X rows of the tile's rows;
+    // apply-right: the X columns of the tile's columns), so the epilogue reads no
+    // X tile.  Only poly still reads an epilogue operand tile (A).
+    constexpr bool kAxInLoop = Tr::kEpilogue == Stage::Apply;
+    constexpr bool kEpiLoad = Tr::kEpiOperand && !kAxInLoop;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * Geo::kStageBytes / 2];
     __shared__ uint32_t s_arrived;
 
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         // (the tile may span several slots from slot 0), rows/cols outside the
         // matrix read as zero.
         auto issue_epi = [&](int eslot) {
-            if constexpr (Tr::kEpiOperand) {
+            if constexpr (kEpiLoad) {
                 const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
                 constexpr int kChunksPerRow = BN / 8;
 #pragma unroll
@@ -346,6 +352,63 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                     fc[j] = frag_kc(bs, wc * WN + j * 32 + (lane & 31), kk, lane);
             }
         };
+        // a·X into the accumulators from the panel of global K-step kg in `slot`,
+        // when that step's 64 K-values are 64 of this tile's rows (apply: X rows;
+        // the column panel [64][BN] holds X[k][col0 + c]) or columns (apply-right:
+        // X columns; the row panel [BM][64] holds X[row0 + r][k]).  Each lane adds
+        // the 4 consecutive values its accumulator elements 4q..4q+3 cover, once
+        // per output element over the whole K loop.
+        auto add_ax = [&](int slot, int kg) {
+            if constexpr (kAxInLoop) {
+                const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
+                const uint16_t *bs = as + Geo::kABytes / 2;
+                const float a = g.s_epi;
+                auto fma4 = [&](f32x16 &acc_ij, int q, u32x2 v) {
+                    float x[4];
+                    unpack4(v, x);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) acc_ij[4 * q + t] = fmaf(a, x[t], acc_ij[4 * q + t]);
+                };
+                if constexpr (S == Stage::Apply) {
+                    const int rel = kg * kBK - row0;  // tile row of the step's first K-row
+                    if (rel < 0 || rel >= BM) return;
+#pragma unroll
+                    for (int i = 0; i < SM; ++i) {
+                        const int rb = wr * WM + 32 * i;
+                        if (rb < rel || rb >= rel + kBK) continue;
+                        const int kr = rb - rel + (lane & 31);
+#pragma unroll
+                        for (int j = 0; j < SN; ++j)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const int c = wc * WN + 32 * j + 8 * q + 4 * (lane >> 5);
+                                fma4(acc[i][j], q,
+                                     *reinterpret_cast<const u32x2 *>(
+                                         bs + nc_offset<BN>(kr, c >> 3) + (c & 7)));
+                            }
+                    }
+                } else {
+                    const int rel = kg * kBK - col0;  // tile column of the step's first K
+                    if (rel < 0 || rel >= BN) return;
+#pragma unroll
+                    for (int j = 0; j < SN; ++j) {
+                        const int cb = wc * WN + 32 * j;
+                        if (cb < rel || cb >= rel + kBK) continue;
+#pragma unroll
+                        for (int i = 0; i < SM; ++i) {
+                            const int r = wr * WM + 32 * i + (lane & 31);
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const int kc = cb - rel + 8 * q + 4 * (lane >> 5);
+                                fma4(acc[i][j], q,
+                                     *reinterpret_cast<const u32x2 *>(
+                                         as + kc_offset(r, kc >> 3) + (kc & 7)));
+                            }
+                        }
+                    }
+                }
+            }
+        };
         auto mfmas = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN]) {
 #pragma unroll
             for (int i = 0; i < SM; ++i)
@@ -380,7 +443,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         // no panel (k = nkl - kStages) issues the epilogue operand tile into its
         // slot instead; every later wait lets those loads stay in flight.
         const int nkl = kend - kbeg;
-        constexpr bool kEpiPrefetch = Tr::kEpiOperand && Geo::kEpiInSlot;
+        constexpr bool kEpiPrefetch = kEpiLoad && Geo::kEpiInSlot;
         bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
         const int npro = nkl < kStages ? nkl : kStages;
         for (int i = 0; i < npro; ++i) issue_all(kbeg + i, i);
@@ -401,6 +464,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         int slot = 0;
         for (int k = 0; k < nkl; ++k) {
             const int next = slot + 1 == kStages ? 0 : slot + 1;
+            if constexpr (kAxInLoop) add_ax(slot, kbeg + k);
             load_frags(slot, 1, fr1, fc1);
             __builtin_amdgcn_sched_barrier(0);
             mfmas(fr0, fc0);
@@ -550,7 +614,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         uint16_t *out = g.out + bt * g.sb_out;
         const bool diag = Tr::kSymmetric && (tm == tn);
 
-        if constexpr (Tr::kEpiOperand && !kEpiPrefetch) {
+        if constexpr (kEpiLoad && !kEpiPrefetch) {
             issue_epi(0);
             wait_vm_barrier<0>();
         }
@@ -566,9 +630,14 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                     const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
                     u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
                     float e[4] = {0.f, 0.f, 0.f, 0.f};
-                    if constexpr (Tr::kEpiOperand) unpack4(*p, e);
                     uint16_t h[4];
-                    epilogue_values<S>(acc[i][j], q, e, g, h);
+                    if constexpr (kAxInLoop) {
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) h[t] = f32_to_bf16_bits(acc[i][j][4 * q + t]);
+                    } else {
+                        if constexpr (kEpiLoad) unpack4(*p, e);
+                        epilogue_values<S>(acc[i][j], q, e, g, h);
+                    }
                     *p = pack4(h);
                 }
             }
