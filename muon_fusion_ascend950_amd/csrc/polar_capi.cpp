@@ -55,7 +55,8 @@ size_t align256(size_t v) { return (v + 255u) & ~size_t(255u); }
 struct Knobs {
     uint32_t gram_tile, poly_tile, apply_bm, apply_bn;
     uint32_t stream;    // 1: DMA-fed kernels where eligible; 0: register-staged kernels only
-    uint32_t stream_k;  // 1: stream-K split of a partial last round (polar_step only); 0: off
+    uint32_t stream_k;  // stream-K split of a partial last round (polar_step only), per stage:
+                        // bit 0 gram, bit 1 poly, bit 2 apply (0: off everywhere)
     uint32_t waves;     // waves per workgroup of the 256x256 DMA-fed kernels (4 or 8)
     uint32_t depth[3];  // LDS ring slots of each stage's DMA-fed kernel (0: by shape)
     bool operator==(const Knobs &o) const {
@@ -187,8 +188,13 @@ int read_knobs(int64_t m, int64_t n, Knobs &k) {
     k.apply_bn = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_N", k.apply_bm));
     k.stream = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM", 1));
     if (k.stream > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM must be 0 or 1");
+    // MUON_POLAR_STREAM_K: 0 off, 1 on (every stage); MUON_POLAR_STREAM_K_STAGES
+    // narrows it to a stage mask (bit 0 gram, bit 1 poly, bit 2 apply).
     k.stream_k = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM_K", 1));
     if (k.stream_k > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM_K must be 0 or 1");
+    const uint64_t sk_stages = env_u64("MUON_POLAR_STREAM_K_STAGES", 7);
+    if (sk_stages > 7) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM_K_STAGES must be 0..7");
+    k.stream_k *= static_cast<uint32_t>(sk_stages);
     k.waves = static_cast<uint32_t>(env_u64("MUON_POLAR_WAVES", kDefaultWaves));
     if (k.waves != 4 && k.waves != 8)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_WAVES must be 4 or 8");
@@ -304,7 +310,7 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
         cus = 0;
     p.pad = p.stream && !tall && n % 8 != 0;
     p.np = p.pad ? round_up(n, 8) : n;
-    const bool sk_ok = p.stream && knobs.stream_k != 0 && (n % 8 == 0 || p.pad) && cus > 0;
+    const bool sk_ok = p.stream && (n % 8 == 0 || p.pad) && cus > 0;
     const int tiles_bm[3] = {p.gram_tile, p.poly_tile, p.apply_bm};
     const int tiles_bn[3] = {p.gram_tile, p.poly_tile, p.apply_bn};
     const Stage stages[3] = {tall ? Stage::GramT : Stage::Gram, Stage::Poly,
@@ -328,7 +334,8 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
                         "others: 2)");
     }
     for (int s = 0; s < 3; ++s) {
-        const int occ = sk_ok ? muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s],
+        const bool sk_stage = sk_ok && (knobs.stream_k >> s & 1u) != 0;
+        const int occ = sk_stage ? muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s],
                                                                  tiles_bn[s], p.waves[s],
                                                                  p.depth[s])
                               : 0;

@@ -436,6 +436,8 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
 
         // Schedule per K-step k (slot k % kStages), slices s0..s3 of 16 K-values:
         //   frags(s1) | mfma(s0) | frags(s2) | mfma(s1) | frags(s3) | mfma(s2) |
+        // (within each "frags(s+1) | mfma(s)" pair the fragment reads are issued
+        // one after each MFMA, 1-2% faster than all reads first at 4096 x 14336)
         //   wait panel k+1, barrier | frags(next s0) | mfma(s3) + DMA panel k+kStages -> slot
         // The barrier sits where every wave has read all of step k's slot into
         // registers; panels k+2 .. k+kStages-1 may still be in flight there.
@@ -466,16 +468,25 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             const int next = slot + 1 == kStages ? 0 : slot + 1;
             if constexpr (kAxInLoop) add_ax(slot, kbeg + k);
             load_frags(slot, 1, fr1, fc1);
-            __builtin_amdgcn_sched_barrier(0);
             mfmas(fr0, fc0);
+            for (int z = 0; z < kMfmaPerSlice; ++z) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
             load_frags(slot, 2, fr0, fc0);
-            __builtin_amdgcn_sched_barrier(0);
             mfmas(fr1, fc1);
+            for (int z = 0; z < kMfmaPerSlice; ++z) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
             load_frags(slot, 3, fr1, fc1);
-            __builtin_amdgcn_sched_barrier(0);
             mfmas(fr0, fc0);
+            for (int z = 0; z < kMfmaPerSlice; ++z) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
             // Wait for panel k+1; panels k+2 .. min(k+kStages-1, nkl-1) (and the
             // epilogue tile once issued) may stay in flight.  Unconditional, also
