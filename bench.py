@@ -209,6 +209,8 @@ def main() -> int:
     ap.add_argument("--profile", action="store_true",
                     help="only the headline step loop and three 1 GiB device copies (the "
                          "calibration kernel of known size), for rocprofv3 runs")
+    ap.add_argument("--profile-secondary", action="store_true",
+                    help="only the [8,512,2048] step loop, for rocprofv3 runs")
     ap.add_argument("--profile-muon", action="store_true",
                     help="only a loop of Muon updates of one fp32 [4096,14336] parameter, "
                          "for rocprofv3 runs")
@@ -235,6 +237,12 @@ def main() -> int:
                                                 weight_decay=MUON_WD), args.steps, args.warmup)
         print(json.dumps({"profile": "muon_update fp32 [4096,14336]", "steps": args.steps,
                           "us_per_update": round(sec * 1e6, 2)}), flush=True)
+        return 0
+    if args.profile_secondary:
+        x2 = make_input(SECONDARY, seed=0).cuda()
+        sec = time_calls(lambda: mf.polar_step(x2, a, b, c), args.steps, args.warmup)
+        print(json.dumps({"profile": "polar_step [8,512,2048]", "steps": args.steps,
+                          "us_per_step": round(sec * 1e6, 2)}), flush=True)
         return 0
     x = make_input((m, n), seed=0).cuda()
     if args.profile:
