@@ -357,7 +357,61 @@ def test_tile_configuration_does_not_change_results(monkeypatch, stream, env):
     assert torch.equal(base, other)
 
 
-@pytest.mark.parametrize("shape", [(8, 512, 2048), (1, 1000, 3000), (3, 200, 264), (2, 64, 4096)])
+@pytest.mark.parametrize("env", [
+    {"MUON_POLAR_GRAM_TILE": "64", "MUON_POLAR_POLY_TILE": "64", "MUON_POLAR_APPLY_TILE_M": "64",
+     "MUON_POLAR_GRAM_DEPTH": "4", "MUON_POLAR_POLY_DEPTH": "8", "MUON_POLAR_APPLY_DEPTH": "2"},
+    {"MUON_POLAR_GRAM_TILE": "64", "MUON_POLAR_POLY_TILE": "64", "MUON_POLAR_APPLY_TILE_M": "64",
+     "MUON_POLAR_GRAM_DEPTH": "8", "MUON_POLAR_POLY_DEPTH": "2", "MUON_POLAR_APPLY_DEPTH": "4"},
+    {"MUON_POLAR_GRAM_TILE": "128", "MUON_POLAR_APPLY_TILE_M": "128",
+     "MUON_POLAR_GRAM_DEPTH": "4", "MUON_POLAR_POLY_DEPTH": "4", "MUON_POLAR_APPLY_DEPTH": "4"},
+    {"MUON_POLAR_APPLY_TILE_M": "256", "MUON_POLAR_APPLY_TILE_N": "128", "MUON_POLAR_APPLY_DEPTH": "3"},
+    {"MUON_POLAR_APPLY_TILE_M": "128", "MUON_POLAR_APPLY_TILE_N": "256", "MUON_POLAR_APPLY_DEPTH": "3"},
+])
+@pytest.mark.parametrize("shape", [(2, 300, 1000), (3, 100, 333)])
+def test_ring_depth_does_not_change_results(monkeypatch, env, shape):
+    """The LDS ring depth changes how many panels are in flight, not what is summed or in
+    which order: results are bit-identical to the default depth (unsplit), including the
+    4-slot epilogue-tile prefetch of the poly stage and the padded route of odd widths."""
+    monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
+    x = O.make_input(shape, seed=21).to(DEV)
+    base = polar_step(x, *C0)
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    other = polar_step(x, *C0)
+    torch.cuda.synchronize()
+    assert torch.equal(base, other)
+
+
+def test_ring_depth_rejects_missing_kernel(monkeypatch):
+    monkeypatch.setenv("MUON_POLAR_GRAM_TILE", "256")
+    monkeypatch.setenv("MUON_POLAR_GRAM_DEPTH", "4")
+    x = O.make_input((1, 300, 1000), seed=22).to(DEV)
+    with pytest.raises(RuntimeError, match="DEPTH"):
+        polar_step(x, *C0)
+
+
+@pytest.mark.parametrize("shape", [(1, 256, 1024), (2, 150, 2050)])
+def test_unaligned_output_pointer(shape):
+    """Y at an address that is not 16-byte aligned (a view one element into a buffer) takes
+    the 2-byte store path of the DMA-fed apply kernel: same bits as an aligned Y."""
+    from muon_fusion_ascend950_amd import capi
+
+    a, b, c = C0
+    x = O.make_input(shape, seed=23).to(DEV)
+    ws, _ = capi.alloc_workspace(*shape)
+    y = torch.empty_like(x)
+    capi.step(x, y, ws, a, b, c)
+    flat = torch.full((x.numel() + 1,), float("nan"), dtype=torch.bfloat16, device=DEV)
+    y_off = flat[1:].view(x.shape)
+    assert y_off.data_ptr() % 16 != 0
+    capi.step(x, y_off, ws, a, b, c)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_off)
+    assert torch.isnan(flat[0])  # nothing written before the view
+
+
+@pytest.mark.parametrize("shape", [(8, 512, 2048), (1, 1000, 3000), (3, 200, 264), (2, 64, 4096),
+                                   (2, 300, 1001), (1, 130, 4099)])
 def test_streaming_and_staged_kernels_agree(monkeypatch, shape):
     """DMA-fed kernels (diagonal-MFMA epilogue terms) and register-staged kernels
     (fma epilogues) agree to bf16 precision, and each matches the oracle."""
