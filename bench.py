@@ -36,7 +36,54 @@ PEAK_HBM_GBS = 8000.0
 COEFFS = (8.156554524902461, -22.48329292557795, 15.878769915207462)  # tests/test_polar_step.py:14
 HEADLINE = (1, 4096, 14336)
 SECONDARY = (8, 512, 2048)
+# Every BASELINE.json configuration on the GPU: (config, shape, steps per call).  Config 0 is
+# the reference's CPU plumbing case, timed here on the GPU as well; five-step calls chain the
+# five coefficient triples (polar_express without normalisation = five polar_step calls).
+CONFIGS = (
+    ("cfg0", (129, 130), 1),
+    ("cfg1", (2, 150, 2050), 1),
+    ("cfg2", (8, 512, 2048), 1),
+    ("cfg3", (8, 512, 2048), 5),
+    ("cfg4", (4096, 14336), 1),
+    ("cfg4", (4096, 14336), 5),
+    ("cfg4", (14336, 4096), 1),
+    ("cfg4", (14336, 4096), 5),
+    ("cfg4", (4, 4096, 4096), 1),
+    ("cfg4", (4, 4096, 4096), 5),
+)
 TRAFFIC_SUMMARY = ROOT / "profiles" / "apply_4096x14336_hbm_traffic.txt"
+
+
+def config_call(shape, steps: int):
+    """The GPU call of one configuration: one polar_step, or the five-step chain."""
+    import torch
+    import muon_fusion_ascend950_amd as mf
+
+    x = make_input(shape, seed=0).cuda()
+    if steps == 1:
+        a, b, c = COEFFS
+        return (lambda: mf.polar_step(x, a, b, c)), x
+    coeffs = mf.COEFFICIENTS[:steps]
+    return (lambda: mf.polar_express(x, coeffs, normalize=False)), x
+
+
+def all_configs(calls_budget_s: float = 0.25):
+    """µs per call and credited TFLOP/s (% of the dense bf16 peak) of every configuration."""
+    rows = []
+    for name, shape, steps in CONFIGS:
+        fn, x = config_call(shape, steps)
+        batch = shape[0] if len(shape) == 3 else 1
+        m, n = shape[-2], shape[-1]
+        once = time_calls(fn, 3, 2)
+        calls = max(5, min(200, int(calls_budget_s / max(once, 1e-6))))
+        sec = time_calls(fn, calls, 3)
+        flops = steps * credited_flops(batch, m, n)
+        rows.append({"config": name, "shape": list(shape), "steps_per_call": steps,
+                     "us_per_call": round(sec * 1e6, 2),
+                     "tflops": round(flops / sec / 1e12, 2),
+                     "pct_bf16_peak": round(100 * flops / sec / 1e12 / PEAK_BF16_TFLOPS, 2)})
+        del x
+    return rows
 
 
 def credited_flops(batch: int, m: int, n: int) -> int:
@@ -211,6 +258,9 @@ def main() -> int:
                          "calibration kernel of known size), for rocprofv3 runs")
     ap.add_argument("--profile-secondary", action="store_true",
                     help="only the [8,512,2048] step loop, for rocprofv3 runs")
+    ap.add_argument("--profile-configs", action="store_true",
+                    help="only a few calls of every BASELINE configuration in turn, for rocprofv3 "
+                         "counter runs")
     ap.add_argument("--profile-muon", action="store_true",
                     help="only a loop of Muon updates of one fp32 [4096,14336] parameter, "
                          "for rocprofv3 runs")
@@ -237,6 +287,14 @@ def main() -> int:
                                                 weight_decay=MUON_WD), args.steps, args.warmup)
         print(json.dumps({"profile": "muon_update fp32 [4096,14336]", "steps": args.steps,
                           "us_per_update": round(sec * 1e6, 2)}), flush=True)
+        return 0
+    if args.profile_configs:
+        for name, shape, steps in CONFIGS:
+            fn, x = config_call(shape, steps)
+            sec = time_calls(fn, args.steps, args.warmup)
+            print(json.dumps({"profile": name, "shape": list(shape), "steps_per_call": steps,
+                              "us_per_call": round(sec * 1e6, 2)}), flush=True)
+            del x
         return 0
     if args.profile_secondary:
         x2 = make_input(SECONDARY, seed=0).cuda()
@@ -355,6 +413,7 @@ def main() -> int:
             "speedup_vs_torch_eager": round(eager2 / sec2, 3),
         },
     }
+    result["all_configs"] = all_configs()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
