@@ -141,30 +141,42 @@ struct Plan {
 std::mutex g_plan_mutex;
 std::unordered_map<PlanKey, Plan, PlanKeyHash> g_plans;
 
-// Default tile shapes by matrix size (measured on MI355X).  256x256 tiles run
-// with 8 waves (two per SIMD: one wave's LDS and barrier waits are covered by
-// the other's MFMAs), 12% faster per step than 4 waves at 4096 x 14336.  The
-// gram stage uses them from m = 3072 (its K = n is long), the poly stage from
-// m = 4096; below that, 128x128 tiles (two workgroups per CU) are faster (2x
-// at m = 2048, where a 256x256 grid has too few tiles; poly at m = 3072: 54 vs
-// 82 us).  Stage 3 has 4x more tiles and prefers 256x256 from m = 1024.  Small
-// matrices use 64x64 tiles to put enough workgroups on the 256 CUs.
+// Default tile shapes (measured on MI355X).  256x256 tiles run with 8 waves
+// (two per SIMD: one wave's LDS and barrier waits are covered by the other's
+// MFMAs).  The symmetric stages use them for large m only — gram from m = 3072
+// (its K = n is long, so stream-K shares stay long), poly from m = 4096 —
+// and otherwise 128x128 tiles (two workgroups per CU) when the batch has at
+// least half a tile per CU of them, else 64x64 ([1, 1024, 4096]: 64x64 gram and
+// poly tiles and 128x128 apply tiles take the step from 89.8 to 54.8 us; at
+// m = 2048, 128x128 is 2x faster than 256x256).  Stage 3 takes the largest of
+// 256x256 and 128x128 that gives every CU a tile, else 64x64.
 constexpr uint32_t kDefaultWaves = 8;
 
-uint32_t default_gram_tile(int64_t m) {
-    if (m >= 3072) return 256;
-    if (m > 512) return 128;
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+uint32_t default_sym_tile(int64_t batch, int64_t s, int64_t large_from, int cus) {
+    if (s >= large_from) return 256;
+    const int64_t t = ceil_div(s, 128);
+    if (batch * (t * (t + 1) / 2) * 2 >= cus) return 128;
     return 64;
 }
-uint32_t default_poly_tile(int64_t m) {
-    if (m >= 4096) return 256;
-    if (m > 512) return 128;
+uint32_t default_apply_tile(int64_t batch, int64_t m, int64_t n, int cus) {
+    for (int64_t t : {256, 128})
+        if (batch * ceil_div(m, t) * ceil_div(n, t) >= cus) return static_cast<uint32_t>(t);
     return 64;
 }
-uint32_t default_apply_tile(int64_t m) {
-    if (m >= 1024) return 256;
-    if (m > 256) return 128;
-    return 64;
+
+// Compute units of `device` (cached; 256 when it cannot be queried).
+int device_cus(int device) {
+    static std::atomic<int> cache[64];
+    if (device < 0 || device >= 64) return 256;
+    int v = cache[device].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        v <= 0)
+        return 256;
+    cache[device].store(v, std::memory_order_relaxed);
+    return v;
 }
 
 // LDS ring depth by shape.  Four slots where they cost no parallelism: 64x64
@@ -177,14 +189,18 @@ int default_depth(int bm, int bn, int64_t tiles, int cus) {
     return 2;
 }
 
-int read_knobs(int64_t m, int64_t n, Knobs &k) {
-    (void)n;
-    k.gram_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_TILE", default_gram_tile(m)));
+// X is [batch, m, n]; s = min(m, n) is the extent of A and P.
+int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
+    const int64_t s = std::min(m, n);
+    k.gram_tile = static_cast<uint32_t>(
+        env_u64("MUON_POLAR_GRAM_TILE", default_sym_tile(batch, s, 3072, cus)));
     // an explicit gram tile also sets the poly tile unless that is given too
     const bool gram_set = std::getenv("MUON_POLAR_GRAM_TILE") != nullptr;
     k.poly_tile = static_cast<uint32_t>(
-        env_u64("MUON_POLAR_POLY_TILE", gram_set ? k.gram_tile : default_poly_tile(m)));
-    k.apply_bm = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_M", default_apply_tile(m)));
+        env_u64("MUON_POLAR_POLY_TILE",
+                gram_set ? k.gram_tile : default_sym_tile(batch, s, 4096, cus)));
+    k.apply_bm = static_cast<uint32_t>(
+        env_u64("MUON_POLAR_APPLY_TILE_M", default_apply_tile(batch, m, n, cus)));
     k.apply_bn = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_N", k.apply_bm));
     k.stream = static_cast<uint32_t>(env_u64("MUON_POLAR_STREAM", 1));
     if (k.stream > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM must be 0 or 1");
@@ -261,13 +277,13 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     if (st != MUON_POLAR_OK) return st;
     const bool tall = m > n;
     const int64_t small = std::min(m, n), large = std::max(m, n);
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) device = -1;
     Knobs knobs{};
-    st = read_knobs(small, large, knobs);
+    st = read_knobs(batch, m, n, device_cus(device), knobs);
     if (st != MUON_POLAR_OK) return st;
     if (tall && knobs.gram_tile == 192)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE=192 is not available for m > n");
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess) device = -1;
     const PlanKey key{device, batch, m, n, knobs};
     std::lock_guard<std::mutex> lock(g_plan_mutex);
     const auto found = g_plans.find(key);
