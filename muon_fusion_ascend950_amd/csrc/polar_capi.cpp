@@ -126,9 +126,10 @@ struct Plan {
     bool sk_any;
     int64_t counter_stride;
     size_t counters_offset, partials_offset;
-    // Rows of n % 8 != 0 elements (m <= n): each step first copies X into a
-    // zero-padded [batch, m, np] buffer (np = roundup(n, 8)) at pad_offset, which
-    // the DMA-fed kernels read; Y is stored with 2-byte stores.
+    // n % 64 != 0: each step first copies X into a zero-padded [batch, m, np]
+    // buffer (np = roundup(n, 64)) at pad_offset, which the DMA-fed kernels read
+    // (their K-contiguous panels need rows of whole 64-element K-steps: they apply
+    // no K masks); Y is stored at its own width (2-byte stores for n % 8 != 0).
     bool pad;
     int64_t np;
     size_t pad_offset;
@@ -324,9 +325,9 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     if (device < 0 ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
         cus = 0;
-    p.pad = p.stream && !tall && n % 8 != 0;
-    p.np = p.pad ? round_up(n, 8) : n;
-    const bool sk_ok = p.stream && (n % 8 == 0 || p.pad) && cus > 0;
+    p.pad = p.stream && n % 64 != 0;
+    p.np = p.pad ? round_up(n, 64) : n;
+    const bool sk_ok = p.stream && cus > 0;
     const int tiles_bm[3] = {p.gram_tile, p.poly_tile, p.apply_bm};
     const int tiles_bn[3] = {p.gram_tile, p.poly_tile, p.apply_bn};
     const Stage stages[3] = {tall ? Stage::GramT : Stage::Gram, Stage::Poly,
@@ -481,8 +482,10 @@ int run_gram(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t batc
     g.out_vec = 1;
     g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
     const bool vec = (ldx % 8 == 0) && aligned16(x);
+    // DMA-fed: X rows are K-contiguous panels, read in whole 64-element K-steps
+    const bool dma = vec && ldx % 64 == 0;
     return finish_stage(launch_stage(Stage::Gram, p.gram_tile, p.gram_tile, p.waves[0], p.depth[0],
-                                     p.stream && vec, vec,
+                                     p.stream && dma, vec,
                                      g, batch, p.gram_grid, &p.sk[0], area, stream),
                         stream, "gram");
 }
@@ -555,14 +558,14 @@ int run_apply(const Plan &p, const void *poly, const void *x, int64_t ldx, void 
 
 // Right-Gram stages for m > n (X is [m, n]): G = Xᵀ·X over the n x n upper
 // tiles, both operands read N-contiguous from X's rows (K runs over the m rows).
-int run_gram_t(const Plan &p, const void *x, void *gram, int64_t batch, int64_t m, int64_t n,
-               const SkArea *area, hipStream_t stream) {
+int run_gram_t(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t batch, int64_t m,
+               int64_t n, const SkArea *area, hipStream_t stream) {
     GemmArgs g{};
     g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(x);
     g.out = static_cast<uint16_t *>(gram);
-    g.sb_row = g.sb_col = g.sb_epi = m * n;
+    g.sb_row = g.sb_col = g.sb_epi = m * ldx;
     g.sb_out = p.mp * p.mp;
-    g.ld_row = g.ld_col = g.ld_epi = static_cast<int32_t>(n);
+    g.ld_row = g.ld_col = g.ld_epi = static_cast<int32_t>(ldx);
     g.ld_out = static_cast<int32_t>(p.mp);
     g.row_rows = g.col_rows = static_cast<int32_t>(n);  // output index: columns of X
     g.row_k = g.col_k = static_cast<int32_t>(m);        // contraction: rows of X
@@ -573,7 +576,7 @@ int run_gram_t(const Plan &p, const void *x, void *gram, int64_t batch, int64_t 
     g.s_epi = 0.0f;
     g.s_acc = 1.0f;
     g.out_vec = 1;
-    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
+    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
     return finish_stage(launch_stage(Stage::GramT, p.gram_tile, p.gram_tile, p.waves[0], p.depth[0], true, true,
                                      g, batch, p.gram_grid, &p.sk[0], area, stream),
                         stream, "gram");
@@ -581,15 +584,18 @@ int run_gram_t(const Plan &p, const void *x, void *gram, int64_t batch, int64_t 
 
 // Y = a·X + X·P for m > n: X rows and P rows (P is symmetric) are both
 // K-contiguous; the output [m, n] and the a·X epilogue are stage 3's.
-int run_apply_r(const Plan &p, const void *poly, const void *x, void *y, int64_t batch,
-                int64_t m, int64_t n, double a, const SkArea *area, hipStream_t stream) {
+int run_apply_r(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y,
+                int64_t batch, int64_t m, int64_t n, double a, const SkArea *area,
+                hipStream_t stream) {
     GemmArgs g{};
     g.rowop = g.epi = static_cast<const uint16_t *>(x);
     g.colop = static_cast<const uint16_t *>(poly);
     g.out = static_cast<uint16_t *>(y);
-    g.sb_row = g.sb_epi = g.sb_out = m * n;
+    g.sb_row = g.sb_epi = m * ldx;
+    g.sb_out = m * n;
     g.sb_col = p.mp * p.mp;
-    g.ld_row = g.ld_epi = g.ld_out = static_cast<int32_t>(n);
+    g.ld_row = g.ld_epi = static_cast<int32_t>(ldx);
+    g.ld_out = static_cast<int32_t>(n);
     g.ld_col = static_cast<int32_t>(p.mp);
     g.row_rows = static_cast<int32_t>(m);
     g.row_k = static_cast<int32_t>(n);
@@ -602,9 +608,9 @@ int run_apply_r(const Plan &p, const void *poly, const void *x, void *y, int64_t
     g.tiles_per_batch = p.apply_tm * p.apply_tn;
     g.s_epi = static_cast<float>(a);
     g.s_acc = 1.0f;
-    g.bytes_row = g.bytes_epi = static_cast<uint32_t>(m * n * 2);
+    g.bytes_row = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
     g.bytes_col = static_cast<uint32_t>(p.mp * p.mp * 2);
-    g.out_vec = 1;
+    g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : 0;
     const uint64_t group_default = p.apply_tn >= 32 ? 8 : 4;
     g.group_n = static_cast<int32_t>(
         std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", group_default)));
@@ -629,7 +635,8 @@ int pad_input(const Plan &p, void *workspace, const void *x, int64_t batch, hipS
     if (!p.pad) return MUON_POLAR_OK;
     uint16_t *xp = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + p.pad_offset);
     const int st = finish_stage(
-        muon_polar::launch_pad_rows(static_cast<const uint16_t *>(x), xp, batch * p.m, p.n, stream),
+        muon_polar::launch_pad_rows(static_cast<const uint16_t *>(x), xp, batch * p.m, p.n, p.np,
+                                    stream),
         stream, "pad");
     if (st != MUON_POLAR_OK) return st;
     xs = xp;
@@ -650,12 +657,12 @@ int run_step(const Plan &p, const void *x, void *y, void *workspace, int64_t bat
     int64_t ldx = p.n;
     int st = pad_input(p, workspace, x, batch, stream, xs, ldx);
     if (st != MUON_POLAR_OK) return st;
-    st = p.tall ? run_gram_t(p, x, gram, batch, p.m, p.n, &areas[0], stream)
-                    : run_gram(p, xs, ldx, gram, batch, p.m, p.n, &areas[0], stream);
+    st = p.tall ? run_gram_t(p, xs, ldx, gram, batch, p.m, p.n, &areas[0], stream)
+                : run_gram(p, xs, ldx, gram, batch, p.m, p.n, &areas[0], stream);
     if (st != MUON_POLAR_OK) return st;
     st = run_poly(p, gram, poly, batch, b, c, &areas[1], stream);
     if (st != MUON_POLAR_OK) return st;
-    return p.tall ? run_apply_r(p, poly, x, y, batch, p.m, p.n, a, &areas[2], stream)
+    return p.tall ? run_apply_r(p, poly, xs, ldx, y, batch, p.m, p.n, a, &areas[2], stream)
                   : run_apply(p, poly, xs, ldx, y, batch, p.m, p.n, a, &areas[2], stream);
 }
 

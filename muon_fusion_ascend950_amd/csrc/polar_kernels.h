@@ -113,8 +113,9 @@ hipError_t launch_norm_scale(const uint16_t *x, uint16_t *y, const float *partia
 hipError_t launch_muon_momentum(const float *g, float *buf, uint16_t *x0, float *partial,
                                 int64_t batch, int64_t mn, float w, float beta, bool nesterov,
                                 bool vec, hipStream_t stream);
-// Xp [rows, roundup(n, 8)] = X [rows, n] with zero columns n.. (16-byte aligned xp).
-hipError_t launch_pad_rows(const uint16_t *x, uint16_t *xp, int64_t rows, int64_t n,
+// Xp [rows, np] = X [rows, n] with zero columns n .. np-1 (np >= n, np % 8 == 0,
+// 16-byte aligned xp).
+hipError_t launch_pad_rows(const uint16_t *x, uint16_t *xp, int64_t rows, int64_t n, int64_t np,
                            hipStream_t stream);
 
 // p ← p·decay + alpha·O over `total` elements; vec: total % 8 == 0, 16-byte aligned.

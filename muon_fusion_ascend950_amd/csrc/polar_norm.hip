@@ -17,9 +17,9 @@
 // the iteration and its sums of squares in the normalisation's own order) and
 // the parameter update p = p·(1 − lr·wd) − lr·scale·O.
 //
-// And the row-padding copy that lets rows of any width (n % 8 != 0) reach the
-// DMA-fed stage kernels: X [rows, n] -> Xp [rows, np], np = roundup(n, 8), the
-// columns n .. np-1 zero, one 16-byte chunk of Xp per thread.
+// And the row-padding copy that gives the DMA-fed stage kernels rows of a whole
+// number of 64-element K-steps: X [rows, n] -> Xp [rows, np], np a multiple of 8
+// (of 64 as used), the columns n .. np-1 zero, one 16-byte chunk of Xp per thread.
 #include "polar_kernels.h"
 #include "polar_tile.hpp"
 
@@ -228,30 +228,40 @@ __global__ __launch_bounds__(kNormThreads) void muon_param_update_kernel(
 __global__ __launch_bounds__(kNormThreads) void pad_rows_kernel(const uint16_t *__restrict__ x,
                                                                 uint16_t *__restrict__ xp,
                                                                 int64_t chunks, int32_t n,
-                                                                int32_t row_chunks) {
+                                                                int32_t row_chunks, int32_t vec) {
+    // row_chunks = np / 8: chunks per padded row; vec: 16-byte loads of whole
+    // chunks (n % 8 == 0 and x 16-byte aligned)
     const int64_t stride = int64_t(gridDim.x) * kNormThreads;
     for (int64_t q = int64_t(blockIdx.x) * kNormThreads + threadIdx.x; q < chunks; q += stride) {
         const int64_t r = q / row_chunks;
         const int c0 = static_cast<int>(q - r * row_chunks) * 8;
         const uint16_t *src = x + r * n + c0;
-        uint32_t h[8];
+        u32x4 v;
+        if (vec && c0 + 8 <= n) {
+            v = *reinterpret_cast<const u32x4 *>(src);
+        } else {
+            uint32_t h[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = c0 + e < n ? uint32_t(src[e]) : 0u;
-        *reinterpret_cast<u32x4 *>(xp + q * 8) = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16),
-                                                       h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+            for (int e = 0; e < 8; ++e) h[e] = c0 + e < n ? uint32_t(src[e]) : 0u;
+            v = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                      h[6] | (h[7] << 16)};
+        }
+        *reinterpret_cast<u32x4 *>(xp + q * 8) = v;
     }
 }
 
 }  // namespace
 
-hipError_t launch_pad_rows(const uint16_t *x, uint16_t *xp, int64_t rows, int64_t n,
+hipError_t launch_pad_rows(const uint16_t *x, uint16_t *xp, int64_t rows, int64_t n, int64_t np,
                            hipStream_t stream) {
-    if (rows <= 0 || n <= 0 || n >= (int64_t(1) << 30)) return hipErrorInvalidValue;
-    int32_t row_chunks = static_cast<int32_t>((n + 7) / 8), nn = static_cast<int32_t>(n);
+    if (rows <= 0 || n <= 0 || np < n || np % 8 != 0 || np >= (int64_t(1) << 30))
+        return hipErrorInvalidValue;
+    int32_t row_chunks = static_cast<int32_t>(np / 8), nn = static_cast<int32_t>(n);
     int64_t chunks = rows * row_chunks;
+    int32_t vec = (n % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0) ? 1 : 0;
     const int64_t blocks = (chunks + kNormThreads - 1) / kNormThreads;
     const unsigned grid = static_cast<unsigned>(blocks < 8192 ? blocks : 8192);
-    void *args[] = {&x, &xp, &chunks, &nn, &row_chunks};
+    void *args[] = {&x, &xp, &chunks, &nn, &row_chunks, &vec};
     return hipLaunchKernel(reinterpret_cast<const void *>(&pad_rows_kernel), dim3(grid),
                            dim3(kNormThreads), args, 0, stream);
 }

@@ -131,6 +131,10 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     constexpr bool kAxInLoop = Tr::kEpilogue == Stage::Apply;
     constexpr bool kEpiLoad = Tr::kEpiOperand && !kAxInLoop;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * Geo::kStageBytes / 2];
+    // 1 KiB per wave that the ring's idle DMA instructions write (out-of-range
+    // offsets: zeros, no memory traffic) in the last kStages steps of a segment,
+    // so that every step issues the same instructions: no branch around them.
+    __shared__ __attribute__((aligned(1024))) uint16_t sink[NW * 512];
     __shared__ uint32_t s_arrived;
 
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -263,41 +267,29 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         auto b_step = [&](int k0) -> uint32_t {
             return static_cast<uint32_t>((Tr::kColNC ? k0 * g.ld_col : k0) * 2);
         };
-        // DMA instruction d (0 .. kLoads-1) of K-step `step` into `slot`; `tail`
-        // applies the K-extent masks (only the last K-step can be partial).
-        auto dma_one = [&](int d, int step, int slot, bool tail) {
+        // DMA instruction d (0 .. kLoads-1) of K-step `step` into `slot`, or, when
+        // `live` is false, out-of-range zeros into this wave's sink block (the same
+        // instruction, chosen by scalar operands).  No K masks: the host passes
+        // K-contiguous operands whose rows extend to a multiple of 64 elements with
+        // zeros (padded copies of X, padded A and P), and N-contiguous operands end
+        // at their buffer's num_records, past which the hardware returns zeros.
+        // (An idle instruction whose row is outside the matrix wraps to offset 0:
+        // an in-range read, also into the sink.)
+        const uint32_t sink_base = lds_addr(sink) + wave * 1024;
+        auto dma_one = [&](int d, int step, int slot, bool live) {
             const int k0 = step * kBK;
             if (d < Geo::kLoadsA) {
-                uint32_t v = off_a[d] + a_step(k0);
-                if (tail) {
-                    if constexpr (Tr::kRowNC) {
-                        if (k0 + a_krow(d) >= g.row_k) v = kOob;
-                    } else {
-                        if (k0 + 8 * a_chunk(d) >= g.row_k) v = kOob;
-                    }
-                }
-                dma_16B(rs_row, a_dst(slot, d), v);
+                const uint32_t koff = live ? a_step(k0) : kOob;
+                dma_16B(rs_row, live ? a_dst(slot, d) : sink_base, off_a[d] + koff);
             } else {
                 const int i = d - Geo::kLoadsA;
-                uint32_t v = off_b[i] + b_step(k0);
-                if (tail) {
-                    if constexpr (Tr::kColNC) {
-                        if (k0 + b_krow(i) >= g.col_k) v = kOob;
-                    } else {
-                        if (k0 + 8 * b_chunk(i) >= g.col_k) v = kOob;
-                    }
-                }
-                dma_16B(rs_col, b_dst(slot, i), v);
+                const uint32_t koff = live ? b_step(k0) : kOob;
+                dma_16B(rs_col, live ? b_dst(slot, i) : sink_base, off_b[i] + koff);
             }
         };
-        auto is_tail = [&](int step) {
-            const int k0 = step * kBK;
-            return k0 + kBK > g.row_k || k0 + kBK > g.col_k;
-        };
         auto issue_all = [&](int step, int slot) {
-            const bool tail = is_tail(step);
 #pragma unroll
-            for (int d = 0; d < Geo::kLoads; ++d) dma_one(d, step, slot, tail);
+            for (int d = 0; d < Geo::kLoads; ++d) dma_one(d, step, slot, true);
         };
 
         // Epilogue operand tile (A for poly, X for apply) -> LDS ring slot `eslot`
@@ -420,13 +412,14 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                 for (int j = 0; j < SN; ++j) acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
         };
         // Last slice of a step: its MFMAs with the DMA of panel `step` interleaved,
-        // about kLoads / kMfmaPerSlice instructions after each MFMA (none when
-        // `active` is false; `tail` applies the K-extent masks of a partial panel),
+        // about kLoads / kMfmaPerSlice instructions after each MFMA (into the sink
+        // when `live` is false: the panel would be past the segment's end; a
+        // branch around each DMA instead cost 3-4% of the step at 4096 x 14336),
         // and the next step's slice-0 fragment reads (from slot `nslot`, complete
         // once the step's barrier has passed) issued one after each MFMA too (0.7%
         // faster at 4096 x 14336 than reading them all first).
         auto mfmas_with_dma_frags = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN], int step,
-                                        int slot_, bool active, bool tail, int nslot,
+                                        int slot_, bool live, int nslot,
                                         bf16x8 (&nfr)[SM], bf16x8 (&nfc)[SN]) {
 #pragma unroll
             for (int m = 0; m < kMfmaPerSlice; ++m) {
@@ -437,7 +430,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
 #pragma unroll
                 for (int d = m * Geo::kLoads / kMfmaPerSlice;
                      d < (m + 1) * Geo::kLoads / kMfmaPerSlice; ++d)
-                    if (active) dma_one(d, step, slot_, tail);
+                    dma_one(d, step, slot_, live);
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
@@ -499,20 +492,22 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
-            // Wait for panel k+1; panels k+2 .. min(k+kStages-1, nkl-1) (and the
-            // epilogue tile once issued) may stay in flight.  Unconditional, also
-            // on the last step (nothing is in flight then, and the fragments read
-            // from the stale slot are not used): a branch around these LDS reads
-            // makes the compiler's wait counts on the join below assume none were
-            // issued, and the slice-3 MFMAs would then wait for all of them.
-            const int ahead = nkl - k - 2;
+            // Wait for panel k+1.  The DMA groups issued after it (each step issues
+            // one, to the ring or the sink; the prologue issued npro) may stay in
+            // flight: prologue panels k+2 .. npro-1 and the groups of steps
+            // k+2-kStages .. k-1, at most kStages-2 groups (plus the epilogue tile
+            // once issued).  Unconditional, also on the last step (nothing needed is
+            // in flight then, and the fragments read from the stale slot are not
+            // used): a branch around these LDS reads makes the compiler's wait
+            // counts on the join below assume none were issued, and the slice-3
+            // MFMAs would then wait for all of them.
+            const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
             if (kEpiPrefetch && k > nkl - kStages)
-                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(ahead);
+                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
             else
-                wait_panels_barrier<Geo::kLoads, kStages - 1>(ahead);
-            const bool more = k + kStages < nkl;
-            mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, more,
-                                 more && is_tail(kbeg + k + kStages), next, fr0, fc0);
+                wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
+            mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
+                                 fc0);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (kEpiPrefetch) {
                 if (k == nkl - kStages) issue_epi(epi_slot);
