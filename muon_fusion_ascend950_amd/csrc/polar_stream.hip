@@ -128,7 +128,14 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     // panel holds this tile's own X values (apply: the X rows of the tile's rows;
     // apply-right: the X columns of the tile's columns), so the epilogue reads no
     // X tile.  Only poly still reads an epilogue operand tile (A).
-    constexpr bool kAxInLoop = Tr::kEpilogue == Stage::Apply;
+    // Wave tiles of 128x128 (4 waves on a 256x256 tile) hold 256 accumulator
+    // registers per lane, which fit only as AGPRs: code that works on the
+    // accumulators with vector ALU instructions inside the K loop (a·X) or with
+    // large register buffers (the partial sums of the stream-K fixup) would force
+    // them into VGPRs and spill, so these kernels add a·X in the epilogue and read
+    // partials in small blocks.
+    constexpr bool kBigAcc = (BM / 2) * (BN / (NW / 2)) >= 128 * 128;
+    constexpr bool kAxInLoop = Tr::kEpilogue == Stage::Apply && !kBigAcc;
     constexpr bool kEpiLoad = Tr::kEpiOperand && !kAxInLoop;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * Geo::kStageBytes / 2];
     // 1 KiB per wave that the ring's idle DMA instructions write (out-of-range
@@ -597,26 +604,33 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             // next block's loads in flight while the current one is added.
             auto add_partial = [&](int u, bool assign) {
                 const uint32_t base = lane_base(u);
-                f32x4 x[2][SN * 4];
-                auto load_block = [&](int i, f32x4 (&dst)[SN * 4]) {
+                // blocks of kBlk accumulator tiles (i, j), the next block's loads in
+                // flight while one is added (one row-block of SN tiles; one tile
+                // for the 256-register accumulators)
+                constexpr int kBlk = kBigAcc ? 1 : SN;
+                constexpr int kBlocks = SM * SN / kBlk;
+                f32x4 x[2][kBlk * 4];
+                auto load_block = [&](int blk, f32x4 (&dst)[kBlk * 4]) {
 #pragma unroll
-                    for (int c = 0; c < SN * 4; ++c)
+                    for (int c = 0; c < kBlk * 4; ++c)
                         dst[c] = __builtin_amdgcn_raw_buffer_load_b128(
-                            rs_part, base + (i * SN * 4 + c) * kChunkStride, 0, kSc1);
+                            rs_part, base + (blk * kBlk * 4 + c) * kChunkStride, 0, kSc1);
                 };
                 load_block(0, x[0]);
 #pragma unroll
-                for (int i = 0; i < SM; ++i) {
-                    if (i + 1 < SM) load_block(i + 1, x[(i + 1) & 1]);
+                for (int blk = 0; blk < kBlocks; ++blk) {
+                    if (blk + 1 < kBlocks) load_block(blk + 1, x[(blk + 1) & 1]);
 #pragma unroll
-                    for (int j = 0; j < SN; ++j)
+                    for (int t = 0; t < kBlk; ++t) {
+                        const int ij = blk * kBlk + t, i = ij / SN, j = ij % SN;
 #pragma unroll
                         for (int q = 0; q < 4; ++q)
 #pragma unroll
                             for (int e = 0; e < 4; ++e)
-                                acc[i][j][4 * q + e] = assign ? x[i & 1][j * 4 + q][e]
+                                acc[i][j][4 * q + e] = assign ? x[blk & 1][t * 4 + q][e]
                                                               : acc[i][j][4 * q + e] +
-                                                                    x[i & 1][j * 4 + q][e];
+                                                                    x[blk & 1][t * 4 + q][e];
+                    }
                 }
             };
             if (from_memory) add_partial(u1, true);
