@@ -240,12 +240,14 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 
 // 16 B per lane from rsrc+voffset into LDS at lds_base(wave-uniform) + 16*lane.
 // Issued as inline assembly so the compiler neither reorders LDS traffic around
-// it nor inserts its own waits; the kernels wait with vmcnt explicitly.
+// it nor inserts its own waits (the LDS-DMA builtin makes it wait for the transfer
+// before every later LDS read); the kernels wait with vmcnt explicitly.  The LDS
+// address is an M0 input operand, which the compiler loads itself.
 __device__ __forceinline__ void dma_16B(i32x4 rsrc, uint32_t lds_base, uint32_t voffset) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
                  :
-                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voffset), "s"(rsrc)
-                 : "memory", "m0");
+                 : "v"(voffset), "s"(rsrc), "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
+                 : "memory");
 }
 
 // Wait until at most N vector-memory operations of this wave are outstanding,
