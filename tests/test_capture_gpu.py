@@ -7,8 +7,11 @@
   words carry a launch token: a replay reuses its captured token and finds the zero counts
   its last run left, eager launches on the same workspace in between use other tokens.
 * A workspace full of garbage gives the same bits as a fresh one (no clearing needed).
-* ``torch.library.opcheck``: schema and FakeTensor registration of the op
+* ``torch.library.opcheck``: schema and FakeTensor registration of the ops
   (reference ``_loader.py:41-48``, ``binding.cpp:679``).
+* ``torch.compile`` (``aot_eager`` backend, full graph) traces the Python wrapper and the op
+  through its FakeTensor registration and runs the same kernels: compiled results equal
+  eager ones bit for bit, for the direct, transposing and right-Gram routes.
 * Gram invariants that pin stage 1 without a reference run: ``trace(A) = ‖X‖_F²`` and
   ``diag(A) ≥ 0`` (sums of squares).
 """
@@ -111,6 +114,38 @@ def test_opcheck_schema_and_fake():
     x = O.make_input((2, 64, 256), seed=32).to(DEV)
     torch.library.opcheck(torch.ops.muon_ascend950.polar_step.default, (x, *C0),
                           test_utils=("test_schema", "test_faketensor"))
+    xt = O.make_input((2, 256, 64), seed=33).to(DEV)
+    torch.library.opcheck(torch.ops.muon_ascend950.polar_step_tall.default, (xt, *C0),
+                          test_utils=("test_schema", "test_faketensor"))
+    flat = [float(v) for triple in O.COEFFICIENTS[:2] for v in triple]
+    torch.library.opcheck(torch.ops.muon_ascend950.polar_express.default, (x, flat, True),
+                          test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.parametrize("shape", [(129, 130), (130, 129), (2, 300, 1000), (1000, 64)])
+def test_torch_compile_matches_eager(shape):
+    """Dynamo traces polar_step (checks, the M > N policy, the op through its fake
+    implementation) into one graph; the compiled call launches the same kernels."""
+    import muon_ascend950
+    import muon_fusion_ascend950_amd as mf
+
+    torch._dynamo.reset()
+
+    @torch.compile(backend="aot_eager", fullgraph=True)
+    def step(x):
+        return muon_ascend950.polar_step(x, *C0)
+
+    @torch.compile(backend="aot_eager", fullgraph=True)
+    def express(x):
+        return mf.polar_express(x, O.COEFFICIENTS[:2])
+
+    x = O.make_input(shape, seed=34).to(DEV)
+    y = step(x)
+    z = express(x)
+    torch.cuda.synchronize()
+    assert y.shape == x.shape and y.dtype == torch.bfloat16
+    assert torch.equal(y, muon_ascend950.polar_step(x, *C0))
+    assert torch.equal(z, mf.polar_express(x, O.COEFFICIENTS[:2]))
 
 
 @pytest.mark.parametrize("shape", [(2, 300, 1000), (1, 4096, 14336), (3, 1024, 8192)])
