@@ -697,8 +697,13 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
                 v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
                           hh[6] | (hh[7] << 16)};
             }
-            if (Tr::kSymmetric || g.out_vec) {
+            if (Tr::kSymmetric) {
                 *reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc) = v;
+            } else if (g.out_vec) {
+                // Y is not read again by this step: a non-temporal store keeps it from
+                // displacing operand panels in L2 ([8,512,2048] 46.8 -> 44.4 us; the
+                // large shapes unchanged; A and P, read by the next stage, stay cached)
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc));
             } else {
                 // rows of n % 8 != 0 elements: 2-byte stores up to the last column
                 uint16_t *dst = out + gr * g.ld_out + gc;
