@@ -255,14 +255,20 @@ int check_shape(int64_t batch, int64_t m, int64_t n) {
 // reads and an epilogue, which shorter shares do not pay back.  Measured on
 // MI355X: with 256x256 tiles (256 KiB partials) 16-step shares lose and 20 and
 // more win or break even; 128x128 tiles (64 KiB partials) gain from 10.
+// Also off when the last round already gives over 3/4 of the `cus` compute
+// units a tile: with two workgroups per CU resident, a CU's second workgroup
+// adds about a third to its throughput, so such a round is as good as full and
+// a split only adds fixups ([8,512,2048] gram: 288 tiles of 64x64 on 256 CUs,
+// unsplit 14.4 us against 18.9 us in 512 units; [3,1024,4096] 88 -> 82 us and
+// [8,1024,4096] 185 -> 176 us per step).
 int64_t sk_min_share(int bm, int bn) { return int64_t(bm) * bn >= 256 * 256 ? 20 : 8; }
 
-SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident,
+SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident, int64_t cus,
                   int64_t min_share) {
     SkSplit c{tiles, 0, 0};
     if (!enabled || resident < 8) return c;
     const int64_t rem = tiles % resident;
-    if (rem == 0 || rem * 4 > resident * 3) return c;
+    if (rem == 0 || rem * 4 > resident * 3 || rem * 4 > cus * 3) return c;
     const int64_t units = std::min<int64_t>(resident, rem * 3) / 8 * 8;
     if (units * 2 < rem * 3 || units < 8) return c;
     const int64_t iters = rem * k_steps;
@@ -356,7 +362,7 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
                                                                  tiles_bn[s], p.waves[s],
                                                                  p.depth[s])
                               : 0;
-        p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ,
+        p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ, cus,
                             sk_min_share(tiles_bm[s], tiles_bn[s]));
         if (p.sk[s].sk_units > 0) {
             p.sk_any = true;

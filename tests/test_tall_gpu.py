@@ -78,7 +78,7 @@ def test_unsplit_equals_transposed_path_bitwise(monkeypatch, shape):
 
 
 @pytest.mark.parametrize("split", ["1", "0"])
-@pytest.mark.parametrize("shape", [(1, 14336, 4096), (3, 523, 200), (2, 8192, 1024)])
+@pytest.mark.parametrize("shape", [(1, 14336, 4096), (3, 523, 200), (2, 8192, 768)])
 def test_exact_sums_are_bitwise(monkeypatch, shape, split):
     monkeypatch.setenv("MUON_POLAR_STREAM_K", split)
     batch, m, n = shape
@@ -111,7 +111,7 @@ def test_exact_sums_are_bitwise(monkeypatch, shape, split):
         assert_bits_equal(bits(y[i]), O.f32_to_bf16_bits(yt_ref.T.astype(np.float32)), "Y")
 
 
-@pytest.mark.parametrize("shape", [(1, 14336, 4096), (2, 8192, 1024)])
+@pytest.mark.parametrize("shape", [(1, 14336, 4096), (2, 8192, 768)])
 def test_split_is_deterministic_and_close_to_transposed(shape):
     assert split_in_use(*shape)
     print(f"split tall {shape}", flush=True)
