@@ -137,6 +137,8 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     constexpr bool kBigAcc = (BM / 2) * (BN / (NW / 2)) >= 128 * 128;
     constexpr bool kAxInLoop = Tr::kEpilogue == Stage::Apply && !kBigAcc;
     constexpr bool kEpiLoad = Tr::kEpiOperand && !kAxInLoop;
+    // Fragment schedule: a whole K-step ahead for one MFMA per slice, else one slice.
+    constexpr bool kStepFrags = kMfmaPerSlice == 1;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * Geo::kStageBytes / 2];
     // 1 KiB per wave that the ring's idle DMA instructions write (out-of-range
     // offsets: zeros, no memory traffic) in the last kStages steps of a segment,
@@ -457,7 +459,6 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         // slot instead; every later wait lets those loads stay in flight.
         const int nkl = kend - kbeg;
         constexpr bool kEpiPrefetch = kEpiLoad && Geo::kEpiInSlot;
-        bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
         const int npro = nkl < kStages ? nkl : kStages;
         for (int i = 0; i < npro; ++i) issue_all(kbeg + i, i);
         int epi_slot = 0;
@@ -473,53 +474,110 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         } else {
             wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
         }
-        load_frags(0, 0, fr0, fc0);
         int slot = 0;
-        for (int k = 0; k < nkl; ++k) {
-            const int next = slot + 1 == kStages ? 0 : slot + 1;
-            if constexpr (kAxInLoop) add_ax(slot, kbeg + k);
-            load_frags(slot, 1, fr1, fc1);
-            mfmas(fr0, fc0);
-            for (int z = 0; z < kMfmaPerSlice; ++z) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if constexpr (kStepFrags) {
+            // One MFMA per k16 slice (32x32 wave tiles): a slice's fragment reads
+            // cannot hide behind the single MFMA issued before them, so every slice
+            // would wait out the LDS latency.  Instead all fragments of step k+1 are
+            // read right after step k's barrier, while step k's MFMAs (on fragments
+            // read one step earlier) run.  MFMAs and a·X additions keep the order of
+            // the schedule below, so results are the same bits.
+            bf16x8 ar[4][SM], ac[4][SN], br[4][SM], bc[4][SN];
+            auto read_step = [&](int sl, bf16x8 (&r)[4][SM], bf16x8 (&c)[4][SN]) {
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) load_frags(sl, kk, r[kk], c[kk]);
+            };
+            auto step = [&](int k, const bf16x8 (&r)[4][SM], const bf16x8 (&c)[4][SN],
+                            bf16x8 (&nr)[4][SM], bf16x8 (&nc)[4][SN]) {
+                const int next = slot + 1 == kStages ? 0 : slot + 1;
+                // the same waits as the schedule below: panel k+1, before this
+                // step's DMA group
+                const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+                if (kEpiPrefetch && k > nkl - kStages)
+                    wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
+                else
+                    wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
+                read_step(next, nr, nc);  // stale on the last step, not used
+                __builtin_amdgcn_sched_barrier(0);
+                constexpr int kM = 4 * kMfmaPerSlice;
+                const int dstep = kbeg + k + kStages;
+                const bool live = k + kStages < nkl;
+#pragma unroll
+                for (int m = 0; m < kM; ++m) {
+                    const int kk = m / kMfmaPerSlice, ij = m % kMfmaPerSlice;
+                    acc[ij / SN][ij % SN] =
+                        mfma_32x32x16(c[kk][ij % SN], r[kk][ij / SN], acc[ij / SN][ij % SN]);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int d = m * Geo::kLoads / kM; d < (m + 1) * Geo::kLoads / kM; ++d)
+                        dma_one(d, dstep, slot, live);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if constexpr (kAxInLoop) {
+                    if (k + 1 < nkl) add_ax(next, kbeg + k + 1);
+                }
+                if constexpr (kEpiPrefetch) {
+                    if (k == nkl - kStages) issue_epi(epi_slot);
+                }
+                slot = next;
+            };
+            if constexpr (kAxInLoop) add_ax(0, kbeg);
+            read_step(0, ar, ac);
+            int k = 0;
+            for (; k + 1 < nkl; k += 2) {
+                step(k, ar, ac, br, bc);
+                step(k + 1, br, bc, ar, ac);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            load_frags(slot, 2, fr0, fc0);
-            mfmas(fr1, fc1);
-            for (int z = 0; z < kMfmaPerSlice; ++z) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (k < nkl) step(k, ar, ac, br, bc);
+        } else {
+            bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
+            load_frags(0, 0, fr0, fc0);
+            for (int k = 0; k < nkl; ++k) {
+                const int next = slot + 1 == kStages ? 0 : slot + 1;
+                if constexpr (kAxInLoop) add_ax(slot, kbeg + k);
+                load_frags(slot, 1, fr1, fc1);
+                mfmas(fr0, fc0);
+                for (int z = 0; z < kMfmaPerSlice; ++z) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                load_frags(slot, 2, fr0, fc0);
+                mfmas(fr1, fc1);
+                for (int z = 0; z < kMfmaPerSlice; ++z) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                load_frags(slot, 3, fr1, fc1);
+                mfmas(fr0, fc0);
+                for (int z = 0; z < kMfmaPerSlice; ++z) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // Wait for panel k+1.  The DMA groups issued after it (each step issues
+                // one, to the ring or the sink; the prologue issued npro) may stay in
+                // flight: prologue panels k+2 .. npro-1 and the groups of steps
+                // k+2-kStages .. k-1, at most kStages-2 groups (plus the epilogue tile
+                // once issued).  Unconditional, also on the last step (nothing needed is
+                // in flight then, and the fragments read from the stale slot are not
+                // used): a branch around these LDS reads makes the compiler's wait
+                // counts on the join below assume none were issued, and the slice-3
+                // MFMAs would then wait for all of them.
+                const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+                if (kEpiPrefetch && k > nkl - kStages)
+                    wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
+                else
+                    wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
+                mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
+                                     fc0);
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (kEpiPrefetch) {
+                    if (k == nkl - kStages) issue_epi(epi_slot);
+                }
+                slot = next;
             }
-            __builtin_amdgcn_sched_barrier(0);
-            load_frags(slot, 3, fr1, fc1);
-            mfmas(fr0, fc0);
-            for (int z = 0; z < kMfmaPerSlice; ++z) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            // Wait for panel k+1.  The DMA groups issued after it (each step issues
-            // one, to the ring or the sink; the prologue issued npro) may stay in
-            // flight: prologue panels k+2 .. npro-1 and the groups of steps
-            // k+2-kStages .. k-1, at most kStages-2 groups (plus the epilogue tile
-            // once issued).  Unconditional, also on the last step (nothing needed is
-            // in flight then, and the fragments read from the stale slot are not
-            // used): a branch around these LDS reads makes the compiler's wait
-            // counts on the join below assume none were issued, and the slice-3
-            // MFMAs would then wait for all of them.
-            const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
-            if (kEpiPrefetch && k > nkl - kStages)
-                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
-            else
-                wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
-            mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
-                                 fc0);
-            __builtin_amdgcn_sched_barrier(0);
-            if constexpr (kEpiPrefetch) {
-                if (k == nkl - kStages) issue_epi(epi_slot);
-            }
-            slot = next;
         }
         // All waves are done with the ring (and no DMA is outstanding).
         wait_vm_barrier<0>();
