@@ -50,7 +50,8 @@ struct GemmArgs {
     int32_t total_tiles, per_xcd;   // batch * tiles_per_batch; ceil(dp_tiles / 8)
     uint32_t bytes_row, bytes_col;  // byte extent of one batch matrix of rowop / colop
     uint32_t bytes_epi;             // byte extent of one batch matrix of epi
-    int32_t group_n;                // apply: column tiles per raster group
+    int32_t group_n;                // apply: column tiles per raster group; gram and
+                                    // poly: super-block side of the tile walk
     // Stream-K split of the streaming kernels.  Tiles [0, dp_tiles) run one per
     // workgroup (the first 8 * per_xcd workgroups); tiles [dp_tiles, total_tiles)
     // form sk_iters = (total_tiles - dp_tiles) * k_steps (tile, K-step)

@@ -206,7 +206,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             tm = r / width;
             tn = grp * gn + r % width;
         } else {
-            upper_tile_of(t, g.tiles_m, tm, tn);
+            upper_tile_blocked(t, g.tiles_m, g.group_n, tm, tn);
         }
         const int row0 = tm * BM, col0 = tn * BN;
 

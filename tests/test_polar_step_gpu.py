@@ -382,6 +382,26 @@ def test_ring_depth_does_not_change_results(monkeypatch, env, shape):
     assert torch.equal(base, other)
 
 
+@pytest.mark.parametrize("shape,tile", [((1, 2000, 2048), "128"), ((2, 1100, 1536), "64"),
+                                        ((1, 1300, 1536), "256")])
+def test_tile_walk_does_not_change_results(monkeypatch, shape, tile):
+    """The triangular stages walk their upper tiles row by row or in super-blocks of
+    MUON_POLAR_SYM_GROUP x MUON_POLAR_SYM_GROUP tiles (ragged at the grid's edge): which
+    workgroup computes a tile changes, not the tile's sums, so unsplit results are
+    bit-identical for every block side, and any tile skipped or computed twice would show.
+    16 to 18 tiles per side, so that blocks of 3, 5 and 8 leave ragged edge blocks."""
+    monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
+    monkeypatch.setenv("MUON_POLAR_GRAM_TILE", tile)
+    x = O.make_input(shape, seed=24).to(DEV)
+    monkeypatch.setenv("MUON_POLAR_SYM_GROUP", "1")
+    base = polar_step(x, *C0)
+    for side in ("2", "3", "5", "8", "64"):
+        monkeypatch.setenv("MUON_POLAR_SYM_GROUP", side)
+        other = polar_step(x, *C0)
+        torch.cuda.synchronize()
+        assert torch.equal(base, other), f"block side {side}"
+
+
 def test_ring_depth_rejects_missing_kernel(monkeypatch):
     monkeypatch.setenv("MUON_POLAR_GRAM_TILE", "256")
     monkeypatch.setenv("MUON_POLAR_GRAM_DEPTH", "4")
