@@ -5,19 +5,24 @@
 //
 //   * global -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging, no
 //     ds_write), 1 KiB per wave instruction, swizzle applied on the global side;
-//   * a 2-deep LDS ring: the panel of K-step k+2 streams in while steps k and
-//     k+1 are multiplied; one barrier per K-step, placed so that the MFMA pipe
-//     keeps a k16 slice of work queued across it, and the DMA instructions of
-//     the next panel are interleaved one by one with that slice's MFMAs;
+//   * an LDS ring of D K-step slots (2 for 256x256 tiles; up to 8 for the
+//     latency-bound small tiles): panels k+1 .. k+D-1 stream in while step k is
+//     multiplied; one barrier per K-step, placed so that the MFMA pipe keeps a
+//     k16 slice of work queued across it, and the DMA instructions of the next
+//     panel are interleaved one by one with that slice's MFMAs;
 //   * MFMA operand fragments double-buffered in registers: the LDS reads of
-//     slice s+1 are in flight while slice s is multiplied;
+//     slice s+1 are in flight while slice s is multiplied (with one MFMA per
+//     slice, 64x64 tiles, a whole K-step's reads run one step ahead instead);
+//   * stream-K: an under-full last round is cut into equal K ranges, one per
+//     workgroup, and summed from fp32 partials by the last contributor;
 //   * edge masking by out-of-range buffer offsets (the hardware returns zeros);
 //   * an LDS-staged epilogue: the epilogue operand tile (X or A) is DMA'd into
 //     the freed ring, each lane combines it with its accumulators in place, and
 //     the tile leaves LDS as coalesced 16-byte row chunks (plus the mirrored tile
 //     for the symmetric stages);
 //   * XCD-aware tile order: workgroup w runs on XCD w % 8, so each XCD gets a
-//     contiguous run of tiles that share operand panels in its L2.
+//     contiguous run of tiles that share operand panels in its L2 (apply: runs
+//     of column tiles walked row by row; gram and poly: super-blocks of tiles).
 //
 // Used when every 16-byte chunk of X is either fully inside or fully outside
 // the matrix (n % 8 == 0, 16-byte aligned X and Y); the register-staged kernels
