@@ -593,6 +593,7 @@ int run_gram_t(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t ba
     g.s_acc = 1.0f;
     g.out_vec = 1;
     g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
+    g.group_n = sym_group();
     return finish_stage(launch_stage(Stage::GramT, p.gram_tile, p.gram_tile, p.waves[0], p.depth[0], true, true,
                                      g, batch, p.gram_grid, &p.sk[0], area, stream),
                         stream, "gram");
