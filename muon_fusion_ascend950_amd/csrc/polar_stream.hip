@@ -588,6 +588,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         wait_vm_barrier<0>();
 
         // -------------------------------------------------------- stream-K fixup
+        bool epi_issued = false;
         if (kbeg != 0 || kend != nk) {
             // This tile is cut between units u0 .. u1.  Each contributor but the
             // last stores its fp32 partial and counts itself in; the last one to
@@ -659,6 +660,13 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             // unit's alone now.  Leave a zero count under this launch's token (a
             // replay of the launch reuses the token).
             if (tid == 0) __hip_atomic_store(cnt, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // The epilogue operand tile (poly's A tile, which fills the idle ring) is
+            // fetched now, so that its round trip overlaps the partials' reads
+            // instead of following them.
+            if constexpr (kEpiLoad && !kEpiPrefetch) {
+                issue_epi(0);
+                epi_issued = true;
+            }
             // Own partial first or second in the order: add the others to it in
             // place (x + y == y + x).  Further back: start from p(u1) in memory.
             const bool from_memory = u1 - unit >= 2;
@@ -707,7 +715,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         const bool diag = Tr::kSymmetric && (tm == tn);
 
         if constexpr (kEpiLoad && !kEpiPrefetch) {
-            issue_epi(0);
+            if (!epi_issued) issue_epi(0);
             wait_vm_barrier<0>();
         }
 
