@@ -160,6 +160,21 @@ def test_edge_shapes(shape):
     assert_matches_oracle(y, x, [C0], rel_exact=1e-2)
 
 
+@pytest.mark.parametrize("shape", [(512, 16, 64), (64, 128, 128), (1, 8, 131072), (2, 3, 40000),
+                                   (1, 65536, 8), (3, 20000, 24)])
+def test_extreme_aspect_and_batch(shape):
+    """Many tiny matrices (a grid of thousands of workgroups), and very wide or very tall
+    skinny matrices: one tile per side with a K loop of hundreds or thousands of steps,
+    which the stream-K split cuts over many workgroups (the right-Gram form for the tall
+    ones)."""
+    print(f"extreme {shape}", flush=True)
+    x = O.make_input(shape, seed=5)
+    y = run_steps(x, [C0])
+    assert y.shape == x.shape
+    assert torch.isfinite(y.float()).all()
+    assert_matches_oracle(y, x, [C0], rel_exact=1e-2)
+
+
 # ----------------------------------------------------------------------------- stages via the C ABI
 def _stages(x3: torch.Tensor, b: float, c: float):
     from muon_fusion_ascend950_amd import capi
