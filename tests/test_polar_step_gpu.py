@@ -511,6 +511,21 @@ def test_baseline_shapes(shape, steps):
         torch.testing.assert_close(y.float(), ref16.float(), rtol=6e-2, atol=6e-2)
 
 
+@pytest.mark.parametrize("shape", [(8192, 16384), (2, 6144, 8192)])
+def test_beyond_baseline_shapes(shape):
+    """Larger than any BASELINE shape: the triangular stages run several full rounds of
+    256x256 tiles (528 and 2 x 300 upper tiles on 256 CUs) before a stream-K remainder,
+    which the BASELINE shapes (a partial first round) never exercise.  Against the fp32
+    formula, with the north star's 6e-2 gate and the 1e-2 normwise bound of one step."""
+    print(f"beyond baseline {shape}", flush=True)
+    x = O.make_input(shape, seed=6).to(DEV)
+    y = polar_step(x, *C0)
+    ref32 = _fp32_formula(x, [C0])
+    torch.testing.assert_close(y.float(), ref32, rtol=6e-2, atol=6e-2)
+    rel = ((y.float() - ref32).norm() / ref32.norm()).item()
+    assert rel <= 1e-2, rel
+
+
 def test_svd_property_at_size():
     """One step maps singular values σ -> aσ + bσ³ + cσ⁵ (size-independent check)."""
     gen = torch.Generator().manual_seed(1)
