@@ -30,10 +30,16 @@
  * workspace needs no clearing (any content, graph replays included).  Calls that
  * share one workspace must not overlap (use one workspace per concurrent stream).
  *
- * Rows of n % 8 != 0 elements (m <= n): each step first copies X into a
- * zero-padded [batch, m, roundup(n, 8)] buffer at the end of the workspace, so
- * that the DMA-fed kernels (16-byte global->LDS transfers) serve every width; Y
- * is written at its own width with 2-byte stores.
+ * Rows of n % 64 != 0 elements: each step first copies X into a zero-padded
+ * [batch, m, roundup(n, 64)] buffer at the end of the workspace, so that the
+ * DMA-fed kernels (16-byte global->LDS transfers of whole 64-element K-steps)
+ * serve every width; Y is written at its own width (2-byte stores when
+ * n % 8 != 0).  Shapes whose padded copy would reach 2^30 elements per matrix
+ * are rejected ("matrix too large"), like X itself.
+ *
+ * Buffers: x, y and the workspace must be pairwise disjoint (no in-place call:
+ * every output tile of stage 3 reads X's whole K range while other tiles are
+ * written to Y).
  *
  * All functions are asynchronous on the given HIP stream (launch only, no
  * synchronisation) unless MUON_POLAR_DEBUG_SYNC is set in the environment, in
@@ -97,9 +103,10 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
  * ignored: the stage runs one output tile per workgroup) or a buffer of
  * info.workspace_bytes, the same one muon_polar_step takes (gram / poly may be
  * its A / P areas), which lets the stage use the stream-K split (and, for
- * n % 8 != 0, the padded copy of X) exactly as inside muon_polar_step, so the
- * three calls reproduce the step bit for bit.  The reference's stage launchers likewise take a
- * device-side buffer (their tiling struct).  The stages take m <= n only. */
+ * n % 64 != 0, the padded copy of X) exactly as inside muon_polar_step, so the
+ * three calls reproduce the step bit for bit.  The reference's stage launchers
+ * likewise take a device-side buffer (their tiling struct).  The stages take
+ * m <= n only. */
 
 /* Stage 1: gram[bt] = X[bt]·X[bt]ᵀ into a [batch, padded_rows, padded_rows]
  * bf16 buffer (padding written as zeros).
@@ -115,7 +122,7 @@ int muon_polar_gram(const void *x, void *gram, void *workspace, size_t workspace
 int muon_polar_poly(const void *gram, void *poly, void *workspace, size_t workspace_bytes,
                     int64_t batch, int64_t m, int64_t n, double b, double c, hipStream_t stream);
 
-/* Stage 3: Y = a·X + poly·X.
+/* Stage 3: Y = a·X + poly·X; y must not overlap x or poly.
  * Replaces launch_muon_cube3_fused_lowlevel (csrc/muon_polar_step_binding.cpp:67-68,
  * csrc/muon_polar_unified_ascend950.asc:1535-1540). */
 int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
@@ -160,6 +167,41 @@ int muon_polar_muon_update(void *param, const void *grad, void *momentum_buffer,
                            int64_t n, double momentum, int nesterov, const double *coefficients,
                            int64_t steps, double lr, double weight_decay, double lr_scale,
                            hipStream_t stream);
+
+/* Host-side check of a launch plan (test support; no reference counterpart).
+ * Builds the plan muon_polar_step would use for [batch, m, n] on a device of
+ * `cus` compute units with blocks_per_cu[s] resident workgroups per CU for the
+ * DMA-fed kernel of stage s (0 gram, 1 poly, 2 apply; the occupancy the device
+ * reports), with the tuning variables of the environment, and walks every
+ * workgroup of each stage with the kernels' own schedule functions.  It reports
+ * the byte ranges each stage can store to, relative to the buffer each range
+ * belongs to, next to those buffers' sizes.  No device is touched. */
+typedef struct muon_polar_stage_extent {
+    int32_t tile_m, tile_n, waves, depth;
+    int32_t dma_fed;       /* 1: DMA-fed kernel; 0: register-staged */
+    int32_t k_steps, total_tiles, dp_tiles, sk_units, grid;
+    int32_t coverage_ok;   /* every (tile, K-step) iteration computed by exactly one workgroup */
+    int32_t extents_ok;    /* per-matrix operand byte extents < 2^31 and passed unchanged */
+    int64_t out_lo, out_hi, out_limit;          /* output stores, bytes: [lo, hi) vs buffer size */
+    int64_t partial_lo, partial_hi, partial_limit; /* stream-K partial slots, bytes */
+    int64_t counter_hi, counter_limit;          /* stream-K arrival words used vs reserved */
+} muon_polar_stage_extent;
+
+typedef struct muon_polar_plan_extents {
+    int64_t workspace_bytes;  /* the step's workspace size */
+    int64_t gram_bytes;       /* A at offset 0 and P at poly_offset, each this size */
+    int64_t poly_offset;
+    int64_t counters_offset;  /* 3 stages x counter_stride 64-bit arrival words */
+    int64_t counter_stride;
+    int64_t partials_offset;  /* partial slots up to pad_offset */
+    int64_t pad_offset;       /* padded copy of X, written up to pad_end (0: none) */
+    int64_t pad_end;
+    int64_t y_bytes;          /* size of Y, the apply stage's output */
+    muon_polar_stage_extent stage[3];
+} muon_polar_plan_extents;
+
+int muon_polar_check_plan(int64_t batch, int64_t m, int64_t n, int cus, const int *blocks_per_cu,
+                          muon_polar_plan_extents *out);
 
 /* Detail of the last failure on the calling thread ("" if none).
  * Replaces CheckAcl / aclGetRecentErrMsg (csrc/muon_polar_step_binding.cpp:72-75). */

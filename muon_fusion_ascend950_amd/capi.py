@@ -20,6 +20,7 @@ EXPORTED_FUNCTIONS = (
     "muon_polar_apply",
     "muon_polar_express",
     "muon_polar_muon_update",
+    "muon_polar_check_plan",
     "muon_polar_last_error",
     "muon_polar_version",
 )
@@ -39,6 +40,22 @@ class ShapeInfo(ctypes.Structure):
         ("express_workspace_bytes", ctypes.c_size_t),
         ("muon_workspace_bytes", ctypes.c_size_t),
     ]
+
+
+class StageExtent(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int32) for name in (
+        "tile_m", "tile_n", "waves", "depth", "dma_fed", "k_steps", "total_tiles", "dp_tiles",
+        "sk_units", "grid", "coverage_ok", "extents_ok")] + [
+        (name, ctypes.c_int64) for name in (
+            "out_lo", "out_hi", "out_limit", "partial_lo", "partial_hi", "partial_limit",
+            "counter_hi", "counter_limit")]
+
+
+class PlanExtents(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int64) for name in (
+        "workspace_bytes", "gram_bytes", "poly_offset", "counters_offset", "counter_stride",
+        "partials_offset", "pad_offset", "pad_end", "y_bytes")] + [
+        ("stage", StageExtent * 3)]
 
 
 class CapiError(RuntimeError):
@@ -80,8 +97,11 @@ def load() -> ctypes.CDLL:
     lib.muon_polar_muon_update.argtypes = [vp, vp, vp, vp, sz, i64, i64, i64, dbl, ctypes.c_int,
                                            ctypes.POINTER(ctypes.c_double), i64, dbl, dbl, dbl,
                                            vp]
+    lib.muon_polar_check_plan.argtypes = [i64, i64, i64, ctypes.c_int,
+                                          ctypes.POINTER(ctypes.c_int), ctypes.POINTER(PlanExtents)]
     for name in ("muon_polar_query", "muon_polar_step", "muon_polar_gram", "muon_polar_poly",
-                 "muon_polar_apply", "muon_polar_express", "muon_polar_muon_update"):
+                 "muon_polar_apply", "muon_polar_express", "muon_polar_muon_update",
+                 "muon_polar_check_plan"):
         getattr(lib, name).restype = ctypes.c_int
     lib.muon_polar_last_error.argtypes = []
     lib.muon_polar_last_error.restype = ctypes.c_char_p
@@ -104,6 +124,16 @@ def query(batch: int, m: int, n: int) -> ShapeInfo:
     info = ShapeInfo()
     check("muon_polar_query", load().muon_polar_query(batch, m, n, ctypes.byref(info)))
     return info
+
+
+def check_plan(batch: int, m: int, n: int, cus: int = 256, blocks_per_cu=(1, 1, 1)) -> PlanExtents:
+    """muon_polar_check_plan: store extents of the step's plan for a device of `cus`
+    compute units and the given resident workgroups per CU of each stage's kernel."""
+    out = PlanExtents()
+    occ = (ctypes.c_int * 3)(*blocks_per_cu)
+    check("muon_polar_check_plan", load().muon_polar_check_plan(batch, m, n, cus, occ,
+                                                                ctypes.byref(out)))
+    return out
 
 
 # --------------------------------------------------------------- torch tensor helpers

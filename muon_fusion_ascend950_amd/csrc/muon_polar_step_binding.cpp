@@ -17,6 +17,16 @@
 
 namespace {
 
+// Contiguous copy of x whose data is 16-byte aligned (a fresh allocation always
+// is).  The DMA-fed kernels read X in 16-byte chunks; a contiguous view at an odd
+// offset (e.g. buf[1:].view(...)) would otherwise take the register-staged kernels
+// (m <= n, about 3.5x slower) or be rejected (m > n).
+at::Tensor aligned_contiguous(const at::Tensor &x) {
+    at::Tensor t = x.contiguous();
+    if (reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 != 0) t = t.clone();
+    return t;
+}
+
 at::Tensor MuonPolarStepHip(const at::Tensor &x, double a, double b, double c) {
     TORCH_CHECK(x.defined(), "muon_polar_step: x must be defined");
     TORCH_CHECK(x.device().is_cuda(), "muon_polar_step: x must be a ROCm (HIP) device tensor");
@@ -28,7 +38,7 @@ at::Tensor MuonPolarStepHip(const at::Tensor &x, double a, double b, double c) {
                 "muon_polar_step: current prototype expects M <= N; transpose policy stays "
                 "outside this op");
     const c10::OptionalDeviceGuard device_guard(x.device());
-    const at::Tensor input = x.contiguous();
+    const at::Tensor input = aligned_contiguous(x);
     const int64_t batch = input.size(0), m = input.size(1), n = input.size(2);
 
     muon_polar_shape_info info{};
@@ -44,14 +54,6 @@ at::Tensor MuonPolarStepHip(const at::Tensor &x, double a, double b, double c) {
                          info.workspace_bytes, batch, m, n, a, b, c, stream);
     TORCH_CHECK(st == MUON_POLAR_OK, "muon_polar_step: ", muon_polar_last_error());
     return out;
-}
-
-// Contiguous copy of x whose data is 16-byte aligned (the DMA-fed kernels that
-// run m > n need it; a fresh allocation always is).
-at::Tensor aligned_contiguous(const at::Tensor &x) {
-    at::Tensor t = x.contiguous();
-    if (reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 != 0) t = t.clone();
-    return t;
 }
 
 // One step on X [batch, M, N] with M > N in the right-Gram form
@@ -102,7 +104,7 @@ at::Tensor MuonPolarExpressHip(const at::Tensor &x, at::ArrayRef<double> coeffic
     TORCH_CHECK(!coefficients.empty() || normalize,
                 "muon_polar_express: no coefficients and no normalisation");
     const c10::OptionalDeviceGuard device_guard(x.device());
-    const at::Tensor input = x.size(1) > x.size(2) ? aligned_contiguous(x) : x.contiguous();
+    const at::Tensor input = aligned_contiguous(x);
     const int64_t batch = input.size(0), m = input.size(1), n = input.size(2);
 
     muon_polar_shape_info info{};

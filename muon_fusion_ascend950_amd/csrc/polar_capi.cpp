@@ -13,6 +13,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <climits>
 #include <atomic>
 #include <cmath>
 #include <cstdint>
@@ -22,8 +23,10 @@
 #include <numeric>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "polar_kernels.h"
+#include "polar_schedule.hpp"
 
 namespace {
 
@@ -167,15 +170,15 @@ uint32_t default_apply_tile(int64_t batch, int64_t m, int64_t n, int cus) {
     return 64;
 }
 
-// Compute units of `device` (cached; 256 when it cannot be queried).
+// Compute units of `device` (cached; 0 when it cannot be queried).
 int device_cus(int device) {
     static std::atomic<int> cache[64];
-    if (device < 0 || device >= 64) return 256;
+    if (device < 0 || device >= 64) return 0;
     int v = cache[device].load(std::memory_order_relaxed);
     if (v > 0) return v;
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
         v <= 0)
-        return 256;
+        return 0;
     cache[device].store(v, std::memory_order_relaxed);
     return v;
 }
@@ -279,25 +282,26 @@ SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident
     return c;
 }
 
-int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
-    int st = check_shape(batch, m, n);
-    if (st != MUON_POLAR_OK) return st;
+// Where a plan is built for: the device (its plan-cache key), its compute units
+// (0: unknown, no stream-K split) and, per stage, the DMA-fed kernel's resident
+// workgroups per CU (-1: ask the runtime for the device's value).
+struct Target {
+    int device;
+    int cus;
+    int blocks_per_cu[3];
+};
+
+// Byte extent of one matrix of every buffer a kernel addresses with 32-bit
+// offsets must stay below 2^31: the DMA-fed kernels mark out-of-range chunks with
+// the offset 2^31, which is only out of range for buffers below that size.
+constexpr int64_t kMaxMatrixElems = int64_t(1) << 30;
+
+int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Target &tgt,
+               Plan &out) {
     const bool tall = m > n;
     const int64_t small = std::min(m, n), large = std::max(m, n);
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess) device = -1;
-    Knobs knobs{};
-    st = read_knobs(batch, m, n, device_cus(device), knobs);
-    if (st != MUON_POLAR_OK) return st;
     if (tall && knobs.gram_tile == 192)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE=192 is not available for m > n");
-    const PlanKey key{device, batch, m, n, knobs};
-    std::lock_guard<std::mutex> lock(g_plan_mutex);
-    const auto found = g_plans.find(key);
-    if (found != g_plans.end()) {
-        out = found->second;
-        return MUON_POLAR_OK;
-    }
     Plan p{};
     p.gram_tile = static_cast<int>(knobs.gram_tile);
     p.poly_tile = static_cast<int>(knobs.poly_tile);
@@ -307,9 +311,10 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     p.n = n;
     p.s = small;
     p.tall = tall;
+    (void)large;
     // A and P are tiled by both stage tiles: pad to a common multiple.
     p.mp = round_up(small, std::lcm(p.gram_tile, p.poly_tile));
-    if (p.mp * p.mp >= (int64_t(1) << 30))
+    if (p.mp * p.mp >= kMaxMatrixElems)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "matrix too large (2^30 elements or more)");
     p.gram_nt = static_cast<int>(p.mp / p.gram_tile);
     p.poly_nt = static_cast<int>(p.mp / p.poly_tile);
@@ -325,14 +330,15 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     if (p.gram_grid >= (int64_t(1) << 31) || p.apply_grid >= (int64_t(1) << 31))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "grid too large");
 
-    // Stream-K needs the DMA-fed kernels (X rows of whole 16-byte chunks) and a
-    // device to size the split for.
-    int cus = 0;
-    if (device < 0 ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
-        cus = 0;
+    const int cus = tgt.cus;
     p.pad = p.stream && n % 64 != 0;
     p.np = p.pad ? round_up(n, 64) : n;
+    // the padded copy of X is read with the same 32-bit offsets as X
+    if (m * p.np >= kMaxMatrixElems)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
+                    "matrix too large (its copy padded to a multiple of 64 columns has 2^30 "
+                    "elements or more)");
+    // Stream-K needs the DMA-fed kernels and a device to size the split for.
     const bool sk_ok = p.stream && cus > 0;
     const int tiles_bm[3] = {p.gram_tile, p.poly_tile, p.apply_bm};
     const int tiles_bn[3] = {p.gram_tile, p.poly_tile, p.apply_bn};
@@ -358,17 +364,21 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     }
     for (int s = 0; s < 3; ++s) {
         const bool sk_stage = sk_ok && (knobs.stream_k >> s & 1u) != 0;
-        const int occ = sk_stage ? muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s],
-                                                                 tiles_bn[s], p.waves[s],
-                                                                 p.depth[s])
-                              : 0;
+        int occ = 0;
+        if (sk_stage)
+            occ = tgt.blocks_per_cu[s] >= 0
+                      ? tgt.blocks_per_cu[s]
+                      : muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s], tiles_bn[s],
+                                                         p.waves[s], p.depth[s]);
         p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ, cus,
                             sk_min_share(tiles_bm[s], tiles_bn[s]));
         if (p.sk[s].sk_units > 0) {
             p.sk_any = true;
-            p.counter_stride = std::max<int64_t>(p.counter_stride, p.sk[s].sk_units);
-            partial_bytes = std::max(partial_bytes, size_t(2) * p.sk[s].sk_units * tiles_bm[s] *
-                                                        tiles_bn[s] * sizeof(float));
+            const int64_t sk_tiles = grids[s] - p.sk[s].dp_tiles;
+            p.counter_stride = std::max<int64_t>(p.counter_stride, sk_tiles);
+            partial_bytes = std::max(partial_bytes,
+                                     size_t(muon_polar::sk_slots(p.sk[s].sk_units, sk_tiles)) *
+                                         tiles_bm[s] * tiles_bn[s] * sizeof(float));
         }
     }
     p.counters_offset = 2 * align256(p.gram_bytes);
@@ -384,6 +394,29 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
         align256(size_t(batch) * muon_polar::norm_chunks(m * n) * sizeof(float));
     p.muon_o_offset = p.express_workspace_bytes;
     p.muon_workspace_bytes = p.muon_o_offset + align256(size_t(batch) * m * n * 2u);
+    out = p;
+    return MUON_POLAR_OK;
+}
+
+int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
+    int st = check_shape(batch, m, n);
+    if (st != MUON_POLAR_OK) return st;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) device = -1;
+    const int cus = device_cus(device);
+    Knobs knobs{};
+    st = read_knobs(batch, m, n, cus > 0 ? cus : 256, knobs);
+    if (st != MUON_POLAR_OK) return st;
+    const PlanKey key{device, batch, m, n, knobs};
+    std::lock_guard<std::mutex> lock(g_plan_mutex);
+    const auto found = g_plans.find(key);
+    if (found != g_plans.end()) {
+        out = found->second;
+        return MUON_POLAR_OK;
+    }
+    Plan p{};
+    st = build_plan(batch, m, n, knobs, Target{device, cus, {-1, -1, -1}}, p);
+    if (st != MUON_POLAR_OK) return st;
     g_plans.emplace(key, p);
     out = p;
     return MUON_POLAR_OK;
@@ -406,6 +439,12 @@ int finish_stage(hipError_t launch, hipStream_t stream, const char *stage) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Whether byte ranges [a, a + a_bytes) and [b, b + b_bytes) share a byte.
+bool overlaps(const void *a, size_t a_bytes, const void *b, size_t b_bytes) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + b_bytes && y < x + a_bytes;
+}
+
 // Workspace areas of polar_step's stream-K splits (null when not splitting:
 // the stage entry points have no workspace and run one tile per workgroup).
 struct SkArea {
@@ -416,28 +455,6 @@ struct SkArea {
 // Launch tokens of the stream-K arrival words: a fresh one per launch, so words
 // left by other launches (or never written) count as zero and need no clearing.
 std::atomic<uint32_t> g_launch_token{1};
-
-// Launch one stage: DMA-fed kernel when allowed, register-staged otherwise.
-hipError_t launch_stage(Stage s, int bm, int bn, int waves, int depth, bool stream_ok, bool vec,
-                        GemmArgs &g, int64_t batch, int64_t grid, const SkSplit *sk,
-                        const SkArea *area, hipStream_t stream) {
-    g.total_tiles = static_cast<int32_t>(batch * g.tiles_per_batch);
-    g.k_steps = g.k_loop / 64;
-    g.dp_tiles = g.total_tiles;
-    g.sk_units = 0;
-    g.sk_iters = 0;
-    if (stream_ok && sk != nullptr && area != nullptr && sk->sk_units > 0) {
-        g.dp_tiles = static_cast<int32_t>(sk->dp_tiles);
-        g.sk_units = sk->sk_units;
-        g.sk_iters = sk->sk_iters;
-        g.partials = area->partials;
-        g.counters = area->counters;
-        g.token = g_launch_token.fetch_add(1, std::memory_order_relaxed);
-    }
-    g.per_xcd = (g.dp_tiles + 7) / 8;
-    if (stream_ok) return muon_polar::launch_stream(s, bm, bn, waves, depth, g, stream);
-    return muon_polar::launch_gemm(s, bm, bn, vec, g, static_cast<int>(grid), stream);
-}
 
 SkArea sk_area(const Plan &p, void *workspace, int stage) {
     char *ws = static_cast<char *>(workspace);
@@ -467,7 +484,6 @@ int stage_area(const Plan &p, void *workspace, size_t workspace_bytes, int stage
     return MUON_POLAR_OK;
 }
 
-// x: [batch, m, n] rows `ldx` elements apart (n, or np for the padded copy).
 // Super-block side of the triangular stages' tile walk (MUON_POLAR_SYM_GROUP; 1: row
 // by row).  8x8 blocks of tiles measured 1.5-2.5% faster than row by row at
 // [4096,14336] (771 -> 757 us) and [2,2048,8192] (297 -> 290 us), the same at
@@ -476,9 +492,35 @@ int32_t sym_group() {
     return static_cast<int32_t>(std::min<uint64_t>(64, env_u64("MUON_POLAR_SYM_GROUP", 8)));
 }
 
-int run_gram(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t batch, int64_t m,
-             int64_t n, const SkArea *area, hipStream_t stream) {
-    GemmArgs g{};
+// Column tiles per raster group of the apply stages: 8 for wide X (4096 x 14336:
+// 56 column tiles), 4 for narrower ones (n = 4096: 16 column tiles; 476 vs 498 us).
+int32_t apply_group(const Plan &p) {
+    const uint64_t group_default = p.apply_tn >= 32 ? 8 : 4;
+    return static_cast<int32_t>(
+        std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", group_default)));
+}
+
+// One stage launch: which kernel and its by-value arguments.  The builders below
+// fill it from the plan, prepare_stage adds the work split and launch_stage runs
+// it; muon_polar_check_plan walks the same arguments on the host.
+struct StageLaunch {
+    Stage stage;
+    int sk_index;     // 0 gram, 1 poly, 2 apply: the plan's split and arrival words
+    int bm, bn, waves, depth;
+    bool stream_ok;   // DMA-fed kernel (else register-staged)
+    bool vec;         // register-staged kernel: 16-byte accesses
+    int64_t grid;     // register-staged grid: one workgroup per tile
+    // byte extent of one batch matrix of rowop, colop and epi, in 64 bits (the
+    // GemmArgs fields are 32-bit)
+    int64_t extent[3];
+    GemmArgs g;
+};
+
+// x: [batch, m, n] rows `ldx` elements apart (n, or np for the padded copy).
+StageLaunch gram_launch(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t m,
+                        int64_t n) {
+    StageLaunch L{};
+    GemmArgs &g = L.g;
     g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(x);
     g.out = static_cast<uint16_t *>(gram);
     g.sb_row = g.sb_col = g.sb_epi = m * ldx;
@@ -494,20 +536,25 @@ int run_gram(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t batc
     g.s_epi = 0.0f;
     g.s_acc = 1.0f;
     g.out_vec = 1;
-    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
+    L.extent[0] = L.extent[1] = L.extent[2] = m * ldx * 2;
     g.group_n = sym_group();
     const bool vec = (ldx % 8 == 0) && aligned16(x);
     // DMA-fed: X rows are K-contiguous panels, read in whole 64-element K-steps
     const bool dma = vec && ldx % 64 == 0;
-    return finish_stage(launch_stage(Stage::Gram, p.gram_tile, p.gram_tile, p.waves[0], p.depth[0],
-                                     p.stream && dma, vec,
-                                     g, batch, p.gram_grid, &p.sk[0], area, stream),
-                        stream, "gram");
+    L.stage = Stage::Gram;
+    L.sk_index = 0;
+    L.bm = L.bn = p.gram_tile;
+    L.waves = p.waves[0];
+    L.depth = p.depth[0];
+    L.stream_ok = p.stream && dma;
+    L.vec = vec;
+    L.grid = p.gram_grid;
+    return L;
 }
 
-int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double b, double c,
-             const SkArea *area, hipStream_t stream) {
-    GemmArgs g{};
+StageLaunch poly_launch(const Plan &p, const void *gram, void *poly, double b, double c) {
+    StageLaunch L{};
+    GemmArgs &g = L.g;
     g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(gram);
     g.out = static_cast<uint16_t *>(poly);
     g.sb_row = g.sb_col = g.sb_epi = g.sb_out = p.mp * p.mp;
@@ -521,19 +568,25 @@ int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double 
     g.s_epi = static_cast<float>(b);
     g.s_acc = static_cast<float>(c);
     g.out_vec = 1;
-    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(p.mp * p.mp * 2);
+    L.extent[0] = L.extent[1] = L.extent[2] = p.mp * p.mp * 2;
     g.group_n = sym_group();
-    return finish_stage(launch_stage(Stage::Poly, p.poly_tile, p.poly_tile, p.waves[1], p.depth[1], p.stream,
-                                     true, g,
-                                     batch, p.poly_grid, &p.sk[1], area, stream),
-                        stream, "poly");
+    L.stage = Stage::Poly;
+    L.sk_index = 1;
+    L.bm = L.bn = p.poly_tile;
+    L.waves = p.waves[1];
+    L.depth = p.depth[1];
+    L.stream_ok = p.stream;
+    L.vec = true;
+    L.grid = p.poly_grid;
+    return L;
 }
 
 // x: [batch, m, n] rows `ldx` elements apart (n, or np for the padded copy);
 // y: [batch, m, n] dense.
-int run_apply(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y, int64_t batch,
-              int64_t m, int64_t n, double a, const SkArea *area, hipStream_t stream) {
-    GemmArgs g{};
+StageLaunch apply_launch(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y,
+                         int64_t m, int64_t n, double a) {
+    StageLaunch L{};
+    GemmArgs &g = L.g;
     g.rowop = static_cast<const uint16_t *>(poly);
     g.colop = g.epi = static_cast<const uint16_t *>(x);
     g.out = static_cast<uint16_t *>(y);
@@ -554,29 +607,31 @@ int run_apply(const Plan &p, const void *poly, const void *x, int64_t ldx, void 
     g.tiles_per_batch = p.apply_tm * p.apply_tn;
     g.s_epi = static_cast<float>(a);
     g.s_acc = 1.0f;
-    g.bytes_row = static_cast<uint32_t>(p.mp * p.mp * 2);
-    g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
+    L.extent[0] = p.mp * p.mp * 2;
+    L.extent[1] = L.extent[2] = m * ldx * 2;
     g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : 0;
-    // Column tiles per raster group: 8 for wide X (4096 x 14336: 56 column tiles),
-    // 4 for narrower ones (n = 4096: 16 column tiles; 476 vs 498 us).
-    const uint64_t group_default = p.apply_tn >= 32 ? 8 : 4;
-    g.group_n = static_cast<int32_t>(
-        std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", group_default)));
+    g.group_n = apply_group(p);
     // DMA-fed kernel: X rows of whole 16-byte chunks (Y any alignment: 2-byte
     // stores when out_vec is 0); register-staged kernel: vectors on both or neither.
     const bool xvec = (ldx % 8 == 0) && aligned16(x);
-    const bool vec = xvec && g.out_vec;
-    return finish_stage(launch_stage(Stage::Apply, p.apply_bm, p.apply_bn, p.waves[2], p.depth[2],
-                                     p.stream && xvec, vec,
-                                     g, batch, p.apply_grid, &p.sk[2], area, stream),
-                        stream, "apply");
+    L.stage = Stage::Apply;
+    L.sk_index = 2;
+    L.bm = p.apply_bm;
+    L.bn = p.apply_bn;
+    L.waves = p.waves[2];
+    L.depth = p.depth[2];
+    L.stream_ok = p.stream && xvec;
+    L.vec = xvec && g.out_vec;
+    L.grid = p.apply_grid;
+    return L;
 }
 
 // Right-Gram stages for m > n (X is [m, n]): G = Xᵀ·X over the n x n upper
 // tiles, both operands read N-contiguous from X's rows (K runs over the m rows).
-int run_gram_t(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t batch, int64_t m,
-               int64_t n, const SkArea *area, hipStream_t stream) {
-    GemmArgs g{};
+StageLaunch gram_t_launch(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t m,
+                          int64_t n) {
+    StageLaunch L{};
+    GemmArgs &g = L.g;
     g.rowop = g.colop = g.epi = static_cast<const uint16_t *>(x);
     g.out = static_cast<uint16_t *>(gram);
     g.sb_row = g.sb_col = g.sb_epi = m * ldx;
@@ -592,19 +647,25 @@ int run_gram_t(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t ba
     g.s_epi = 0.0f;
     g.s_acc = 1.0f;
     g.out_vec = 1;
-    g.bytes_row = g.bytes_col = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
+    L.extent[0] = L.extent[1] = L.extent[2] = m * ldx * 2;
     g.group_n = sym_group();
-    return finish_stage(launch_stage(Stage::GramT, p.gram_tile, p.gram_tile, p.waves[0], p.depth[0], true, true,
-                                     g, batch, p.gram_grid, &p.sk[0], area, stream),
-                        stream, "gram");
+    L.stage = Stage::GramT;
+    L.sk_index = 0;
+    L.bm = L.bn = p.gram_tile;
+    L.waves = p.waves[0];
+    L.depth = p.depth[0];
+    L.stream_ok = true;
+    L.vec = true;
+    L.grid = p.gram_grid;
+    return L;
 }
 
 // Y = a·X + X·P for m > n: X rows and P rows (P is symmetric) are both
 // K-contiguous; the output [m, n] and the a·X epilogue are stage 3's.
-int run_apply_r(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y,
-                int64_t batch, int64_t m, int64_t n, double a, const SkArea *area,
-                hipStream_t stream) {
-    GemmArgs g{};
+StageLaunch apply_r_launch(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y,
+                           int64_t m, int64_t n, double a) {
+    StageLaunch L{};
+    GemmArgs &g = L.g;
     g.rowop = g.epi = static_cast<const uint16_t *>(x);
     g.colop = static_cast<const uint16_t *>(poly);
     g.out = static_cast<uint16_t *>(y);
@@ -625,15 +686,88 @@ int run_apply_r(const Plan &p, const void *poly, const void *x, int64_t ldx, voi
     g.tiles_per_batch = p.apply_tm * p.apply_tn;
     g.s_epi = static_cast<float>(a);
     g.s_acc = 1.0f;
-    g.bytes_row = g.bytes_epi = static_cast<uint32_t>(m * ldx * 2);
-    g.bytes_col = static_cast<uint32_t>(p.mp * p.mp * 2);
+    L.extent[0] = L.extent[2] = m * ldx * 2;
+    L.extent[1] = p.mp * p.mp * 2;
     g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : 0;
-    const uint64_t group_default = p.apply_tn >= 32 ? 8 : 4;
-    g.group_n = static_cast<int32_t>(
-        std::max<uint64_t>(1, env_u64("MUON_POLAR_APPLY_GROUP_N", group_default)));
-    return finish_stage(launch_stage(Stage::ApplyR, p.apply_bm, p.apply_bn, p.waves[2], p.depth[2], true, true,
-                                     g, batch, p.apply_grid, &p.sk[2], area, stream),
-                        stream, "apply");
+    g.group_n = apply_group(p);
+    L.stage = Stage::ApplyR;
+    L.sk_index = 2;
+    L.bm = p.apply_bm;
+    L.bn = p.apply_bn;
+    L.waves = p.waves[2];
+    L.depth = p.depth[2];
+    L.stream_ok = true;
+    L.vec = true;
+    L.grid = p.apply_grid;
+    return L;
+}
+
+// Work split of a stage launch: whole tiles one per workgroup, plus the plan's
+// stream-K split when the DMA-fed kernel runs and a stream-K area is given.
+// `token` tags this launch's arrival words.
+void prepare_stage(StageLaunch &L, int64_t batch, const Plan &p, const SkArea *area,
+                   uint32_t token) {
+    GemmArgs &g = L.g;
+    g.bytes_row = static_cast<uint32_t>(L.extent[0]);
+    g.bytes_col = static_cast<uint32_t>(L.extent[1]);
+    g.bytes_epi = static_cast<uint32_t>(L.extent[2]);
+    g.total_tiles = static_cast<int32_t>(batch * g.tiles_per_batch);
+    g.k_steps = g.k_loop / 64;
+    g.dp_tiles = g.total_tiles;
+    g.sk_units = 0;
+    g.sk_iters = 0;
+    const SkSplit &sk = p.sk[L.sk_index];
+    if (L.stream_ok && area != nullptr && sk.sk_units > 0) {
+        g.dp_tiles = static_cast<int32_t>(sk.dp_tiles);
+        g.sk_units = sk.sk_units;
+        g.sk_iters = sk.sk_iters;
+        g.partials = area->partials;
+        g.counters = area->counters;
+        g.token = token;
+    }
+    g.per_xcd = (g.dp_tiles + 7) / 8;
+}
+
+int launch_stage(StageLaunch &L, int64_t batch, const Plan &p, const SkArea *area,
+                 hipStream_t stream, const char *name) {
+    prepare_stage(L, batch, p, area, g_launch_token.fetch_add(1, std::memory_order_relaxed));
+    const hipError_t e =
+        L.stream_ok
+            ? muon_polar::launch_stream(L.stage, L.bm, L.bn, L.waves, L.depth, L.g, stream)
+            : muon_polar::launch_gemm(L.stage, L.bm, L.bn, L.vec, L.g, static_cast<int>(L.grid),
+                                      stream);
+    return finish_stage(e, stream, name);
+}
+
+int run_gram(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t batch, int64_t m,
+             int64_t n, const SkArea *area, hipStream_t stream) {
+    StageLaunch L = gram_launch(p, x, ldx, gram, m, n);
+    return launch_stage(L, batch, p, area, stream, "gram");
+}
+
+int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double b, double c,
+             const SkArea *area, hipStream_t stream) {
+    StageLaunch L = poly_launch(p, gram, poly, b, c);
+    return launch_stage(L, batch, p, area, stream, "poly");
+}
+
+int run_apply(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y, int64_t batch,
+              int64_t m, int64_t n, double a, const SkArea *area, hipStream_t stream) {
+    StageLaunch L = apply_launch(p, poly, x, ldx, y, m, n, a);
+    return launch_stage(L, batch, p, area, stream, "apply");
+}
+
+int run_gram_t(const Plan &p, const void *x, int64_t ldx, void *gram, int64_t batch, int64_t m,
+               int64_t n, const SkArea *area, hipStream_t stream) {
+    StageLaunch L = gram_t_launch(p, x, ldx, gram, m, n);
+    return launch_stage(L, batch, p, area, stream, "gram");
+}
+
+int run_apply_r(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y,
+                int64_t batch, int64_t m, int64_t n, double a, const SkArea *area,
+                hipStream_t stream) {
+    StageLaunch L = apply_r_launch(p, poly, x, ldx, y, m, n, a);
+    return launch_stage(L, batch, p, area, stream, "apply");
 }
 
 // m > n runs only on the DMA-fed kernels.
@@ -704,6 +838,123 @@ int reject_tall_stage(int64_t m, int64_t n) {
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
                     "the stage entry points expect m <= n (muon_polar_step runs m > n)");
     return MUON_POLAR_OK;
+}
+
+// ---------------------------------------------------------------- plan check
+// Host walk of every workgroup of a stage launch (the kernels' own schedule
+// functions, polar_schedule.hpp) that bounds the bytes each can store to: its
+// output tile (and mirrored tile), its stream-K partial slots and arrival word.
+// Addresses are relative to the base pointers in L.g; the caller compares them
+// with the buffers' sizes.
+void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e) {
+    const GemmArgs &g = L.g;
+    const bool sym = L.stage == Stage::Gram || L.stage == Stage::Poly || L.stage == Stage::GramT;
+    e.tile_m = L.bm;
+    e.tile_n = L.bn;
+    e.waves = L.waves;
+    e.depth = L.depth;
+    e.dma_fed = L.stream_ok ? 1 : 0;
+    e.k_steps = g.k_steps;
+    e.total_tiles = g.total_tiles;
+    e.dp_tiles = g.dp_tiles;
+    e.sk_units = g.sk_units;
+    e.grid = L.stream_ok ? g.sk_units + 8 * g.per_xcd : static_cast<int32_t>(L.grid);
+    e.out_lo = INT64_MAX;
+    e.out_hi = 0;
+    e.partial_lo = INT64_MAX;
+    e.partial_hi = 0;
+    e.counter_hi = 0;
+    e.extents_ok = 1;
+    for (int i = 0; i < 3; ++i) {
+        const uint32_t passed = i == 0 ? g.bytes_row : (i == 1 ? g.bytes_col : g.bytes_epi);
+        if (L.extent[i] >= (int64_t(1) << 31) || int64_t(passed) != L.extent[i]) e.extents_ok = 0;
+    }
+    const int nk = g.k_steps;
+    const int64_t slot_bytes = int64_t(L.bm) * L.bn * 4;
+    // (tile, K-step) iterations covered, to show each is computed exactly once
+    std::vector<uint8_t> seen(static_cast<size_t>(g.total_tiles) * nk, 0);
+    bool once = true;
+    auto store_tile = [&](int bt, int row0, int col0) {
+        // element range [lo, hi) of one workgroup's epilogue stores
+        int64_t lo, hi;
+        if (sym) {
+            // whole tile and its mirror, no bounds checks in the kernel
+            const int64_t base = int64_t(bt) * g.sb_out;
+            lo = base + std::min(int64_t(row0) * g.ld_out + col0, int64_t(col0) * g.ld_out + row0);
+            hi = base + std::max(int64_t(row0 + L.bm - 1) * g.ld_out + col0 + L.bn,
+                                 int64_t(col0 + L.bn - 1) * g.ld_out + row0 + L.bm);
+        } else {
+            const int last_row = std::min(row0 + L.bm, g.out_rows) - 1;
+            if (last_row < row0 || col0 >= g.out_cols) return;
+            // last 16-byte chunk that starts inside the matrix; 8-element vector
+            // stores when out_vec, else element stores up to the last column
+            const int last_chunk = col0 + 8 * ((std::min(col0 + L.bn, g.out_cols) - 1 - col0) / 8);
+            const int64_t end_col = g.out_vec ? last_chunk + 8 : std::min(col0 + L.bn, g.out_cols);
+            lo = int64_t(bt) * g.sb_out + int64_t(row0) * g.ld_out + col0;
+            hi = int64_t(bt) * g.sb_out + int64_t(last_row) * g.ld_out + end_col;
+        }
+        e.out_lo = std::min(e.out_lo, lo * 2);
+        e.out_hi = std::max(e.out_hi, hi * 2);
+    };
+    if (!L.stream_ok) {
+        // register-staged kernels: one workgroup per tile
+        for (int64_t w = 0; w < L.grid; ++w) {
+            const int bt = static_cast<int>(w / g.tiles_per_batch);
+            const int t = static_cast<int>(w - int64_t(bt) * g.tiles_per_batch);
+            int tm, tn;
+            if (sym)
+                muon_polar::upper_tile_of(t, g.tiles_m, tm, tn);
+            else {
+                tm = t % g.tiles_m;
+                tn = t / g.tiles_m;
+            }
+            store_tile(bt, tm * L.bm, tn * L.bn);
+            for (int k = 0; k < nk; ++k) once = once && seen[size_t(w) * nk + k]++ == 0;
+        }
+    } else {
+        for (int w = 0; w < e.grid; ++w) {
+            int unit, tile_base;
+            int64_t it_lo, it_hi;
+            if (!muon_polar::workgroup_range(g, w, unit, tile_base, it_lo, it_hi)) continue;
+            for (int64_t hi = it_hi; hi > it_lo;) {
+                const int lt = static_cast<int>((hi - 1) / nk);
+                const int64_t tstart = int64_t(lt) * nk;
+                const int64_t lo = tstart > it_lo ? tstart : it_lo;
+                const int kbeg = static_cast<int>(lo - tstart), kend = static_cast<int>(hi - tstart);
+                hi = lo;
+                const int tlin = tile_base + lt;
+                if (tlin < 0 || tlin >= g.total_tiles) {
+                    once = false;
+                    continue;
+                }
+                for (int k = kbeg; k < kend; ++k) once = once && seen[size_t(tlin) * nk + k]++ == 0;
+                const int bt = tlin / g.tiles_per_batch;
+                int tm, tn;
+                muon_polar::tile_coords(g, sym, tlin - bt * g.tiles_per_batch, tm, tn);
+                store_tile(bt, tm * L.bm, tn * L.bn);
+                if (kbeg != 0 || kend != nk) {
+                    // cut tile: arrival word lt, partial slots of its contributors
+                    if (!splits || unit < 0) {
+                        once = false;
+                        continue;
+                    }
+                    e.counter_hi = std::max<int64_t>(e.counter_hi, lt + 1);
+                    const int u0 = muon_polar::sk_unit_of(g, tstart);
+                    const int u1 = muon_polar::sk_unit_of(g, tstart + nk - 1);
+                    if (unit < u0 || unit > u1) once = false;
+                    for (int u = u0; u <= u1; ++u) {
+                        const int64_t slot = muon_polar::sk_slot(u, lt);
+                        e.partial_lo = std::min(e.partial_lo, slot * slot_bytes);
+                        e.partial_hi = std::max(e.partial_hi, (slot + 1) * slot_bytes);
+                    }
+                }
+            }
+        }
+    }
+    for (uint8_t c : seen) once = once && c == 1;
+    e.coverage_ok = once ? 1 : 0;
+    if (e.out_lo == INT64_MAX) e.out_lo = 0;
+    if (e.partial_lo == INT64_MAX) e.partial_lo = 0;
 }
 
 }  // namespace
@@ -780,6 +1031,12 @@ int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
     const SkArea *ap = nullptr;
     st = stage_area(p, workspace, workspace_bytes, 2, area, ap);
     if (st != MUON_POLAR_OK) return st;
+    // every output tile reads X's whole K range while other tiles write Y
+    const size_t xy_bytes = static_cast<size_t>(batch * m * n * 2);
+    if (overlaps(x, xy_bytes, y, xy_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "x and y must not overlap");
+    if (overlaps(poly, p.gram_bytes, y, xy_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "poly and y must not overlap");
     const void *xs = x;
     int64_t ldx = n;
     if (ap != nullptr) {
@@ -798,10 +1055,19 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
     if (st != MUON_POLAR_OK) return st;
     st = check_workspace(p, workspace, workspace_bytes);
     if (st != MUON_POLAR_OK) return st;
+    // The apply stage reads X's whole K range for every output tile while other
+    // tiles are written to Y, and the workspace holds A, P and the padded X: an
+    // in-place call (y == x), or a workspace over x or y, would race.
     if (p.tall) {
         st = check_tall(p, x, y);
         if (st != MUON_POLAR_OK) return st;
     }
+    const size_t xy_bytes = static_cast<size_t>(batch * m * n * 2);
+    if (overlaps(x, xy_bytes, y, xy_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "x and y must not overlap");
+    if (overlaps(workspace, p.workspace_bytes, x, xy_bytes) ||
+        overlaps(workspace, p.workspace_bytes, y, xy_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "the workspace must not overlap x or y");
     return run_step(p, x, y, workspace, batch, a, b, c, stream);
 }
 
@@ -823,9 +1089,8 @@ int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace
                         " bytes, got " + std::to_string(workspace == nullptr ? 0 : workspace_bytes));
     if (!aligned16(workspace))
         return fail(MUON_POLAR_ERR_WORKSPACE, "workspace must be 16-byte aligned");
-    const uintptr_t xb = reinterpret_cast<uintptr_t>(x), yb = reinterpret_cast<uintptr_t>(y);
-    const uintptr_t bytes = static_cast<uintptr_t>(batch * m * n * 2);
-    if (xb < yb + bytes && yb < xb + bytes)
+    const size_t xy_bytes = static_cast<size_t>(batch * m * n * 2);
+    if (overlaps(x, xy_bytes, y, xy_bytes))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "x and y must not overlap");
     if (p.tall && steps > 0) {
         st = check_tall(p, x, y);
@@ -922,6 +1187,57 @@ int muon_polar_muon_update(void *param, const void *grad, void *momentum_buffer,
             static_cast<float *>(param), out, total, static_cast<float>(1.0 - lr * weight_decay),
             static_cast<float>(-lr * lr_scale), total % 8 == 0 && aligned16(param), stream),
         stream, "param update");
+}
+
+int muon_polar_check_plan(int64_t batch, int64_t m, int64_t n, int cus, const int *blocks_per_cu,
+                          muon_polar_plan_extents *out) {
+    if (out == nullptr || blocks_per_cu == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    if (cus < 0) return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "cus must be >= 0");
+    int st = check_shape(batch, m, n);
+    if (st != MUON_POLAR_OK) return st;
+    Knobs knobs{};
+    st = read_knobs(batch, m, n, cus > 0 ? cus : 256, knobs);
+    if (st != MUON_POLAR_OK) return st;
+    Plan p{};
+    st = build_plan(batch, m, n, knobs,
+                    Target{-1, cus, {blocks_per_cu[0], blocks_per_cu[1], blocks_per_cu[2]}}, p);
+    if (st != MUON_POLAR_OK) return st;
+    *out = muon_polar_plan_extents{};
+    out->workspace_bytes = static_cast<int64_t>(p.workspace_bytes);
+    out->gram_bytes = static_cast<int64_t>(p.gram_bytes);
+    out->poly_offset = static_cast<int64_t>(align256(p.gram_bytes));
+    out->counters_offset = static_cast<int64_t>(p.counters_offset);
+    out->counter_stride = p.counter_stride;
+    out->partials_offset = static_cast<int64_t>(p.partials_offset);
+    out->pad_offset = static_cast<int64_t>(p.pad_offset);
+    out->pad_end = p.pad ? static_cast<int64_t>(p.pad_offset) + batch * m * p.np * 2 : 0;
+    out->y_bytes = batch * m * n * 2;
+    // The step's route on stand-in addresses (16-byte aligned, never dereferenced):
+    // the workspace, X and Y in address ranges of their own.
+    char *ws = reinterpret_cast<char *>(uintptr_t(1) << 44);
+    const uintptr_t kX = uintptr_t(2) << 44, kY = uintptr_t(3) << 44;
+    const void *x = reinterpret_cast<const void *>(kX);
+    void *y = reinterpret_cast<void *>(kY);
+    const void *xs = p.pad ? static_cast<const void *>(ws + p.pad_offset) : x;
+    const int64_t ldx = p.pad ? p.np : n;
+    void *gram = ws;
+    void *poly = ws + align256(p.gram_bytes);
+    StageLaunch L[3] = {p.tall ? gram_t_launch(p, xs, ldx, gram, m, n) : gram_launch(p, xs, ldx, gram, m, n),
+                        poly_launch(p, gram, poly, 1.0, 1.0),
+                        p.tall ? apply_r_launch(p, poly, xs, ldx, y, m, n, 1.0)
+                               : apply_launch(p, poly, xs, ldx, y, m, n, 1.0)};
+    for (int s = 0; s < 3; ++s) {
+        SkArea area{reinterpret_cast<float *>(ws + p.partials_offset),
+                    reinterpret_cast<uint64_t *>(ws + p.counters_offset) + s * p.counter_stride};
+        prepare_stage(L[s], batch, p, &area, 1u);
+        // extents relative to the stage's output buffer, partial area and words
+        stage_extent(L[s], L[s].g.sk_units > 0, out->stage[s]);
+        out->stage[s].out_limit = s == 2 ? out->y_bytes : out->gram_bytes;
+        out->stage[s].partial_limit = out->pad_offset - out->partials_offset;
+        out->stage[s].counter_limit = p.counter_stride;
+    }
+    return MUON_POLAR_OK;
 }
 
 const char *muon_polar_last_error(void) { return g_last_error.c_str(); }

@@ -19,6 +19,7 @@
 // stage-1/2 tile; rows/columns >= m are computed from zero-filled X rows and are
 // therefore exact zeros, so stages 2 and 3 need no K masking on A or P.
 #include "polar_kernels.h"
+#include "polar_schedule.hpp"
 #include "polar_tile.hpp"
 #include "polar_epilogue.hpp"
 

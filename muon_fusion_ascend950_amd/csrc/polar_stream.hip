@@ -29,6 +29,7 @@
 // cover the rest.
 #include "polar_epilogue.hpp"
 #include "polar_kernels.h"
+#include "polar_schedule.hpp"
 #include "polar_tile.hpp"
 
 namespace muon_polar {
@@ -100,22 +101,6 @@ __device__ __forceinline__ int epi_offset(int row, int col) {
     return row * BN + (epi_pos<BN>(row, col >> 3) << 3) + (col & 7);
 }
 
-// Stream-K bookkeeping (all values uniform across the workgroup).
-// Range of unit u: iterations [sk_bound(u), sk_bound(u + 1)).
-__device__ __forceinline__ int64_t sk_bound(const GemmArgs &g, int u) {
-    return int64_t(u) * g.sk_iters / g.sk_units;
-}
-// Unit whose range holds iteration i: the largest u with sk_bound(u) <= i.
-__device__ __forceinline__ int sk_unit_of(const GemmArgs &g, int64_t i) {
-    const int64_t u = ((i + 1) * g.sk_units - 1) / g.sk_iters;
-    return u < g.sk_units ? static_cast<int>(u) : g.sk_units - 1;
-}
-// Partial slot of unit u for stream-K tile st: 2u for the first tile of its
-// range, 2u + 1 for the last one (only those two can be cut).
-__device__ __forceinline__ int sk_slot(const GemmArgs &g, int u, int st) {
-    return 2 * u + (st != static_cast<int>(sk_bound(g, u) / g.k_steps));
-}
-
 template <int BM, int BN, Stage S, int NW, int D>
 __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     using Geo = StreamGeom<BM, BN, NW, D>;
@@ -156,27 +141,11 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     const int nk = g.k_steps;
     const uint32_t smem_base = lds_addr(smem);
 
-    // Work of this workgroup: iterations [it_lo, it_hi) of tiles tile_base + i / nk.
-    // Workgroup w runs on XCD w % 8; each XCD gets a contiguous run of whole
-    // tiles (workgroups [0, 8 * per_xcd), dispatched first, so full rounds start
-    // together and tiles that share operand panels stay in step) and of
-    // stream-K units (the rest, which fill the last round as CUs free up).
-    const int w = blockIdx.x;
-    const int dp_grid = 8 * g.per_xcd;
-    int unit = -1, tile_base;
+    // Work of this workgroup: iterations [it_lo, it_hi) of tiles tile_base + i / nk
+    // (polar_schedule.hpp: XCD-contiguous whole tiles, then the stream-K units).
+    int unit, tile_base;
     int64_t it_lo, it_hi;
-    if (w >= dp_grid) {
-        const int ws = w - dp_grid;
-        unit = (ws & 7) * (g.sk_units >> 3) + (ws >> 3);
-        tile_base = g.dp_tiles;
-        it_lo = sk_bound(g, unit);
-        it_hi = sk_bound(g, unit + 1);
-    } else {
-        tile_base = (w & 7) * g.per_xcd + (w >> 3);
-        if (tile_base >= g.dp_tiles) return;
-        it_lo = 0;
-        it_hi = nk;
-    }
+    if (!workgroup_range(g, static_cast<int>(blockIdx.x), unit, tile_base, it_lo, it_hi)) return;
 
     // Segments are taken from the end of the range backwards: a unit first
     // computes the leading K-steps of its last tile (a partial the tile's owner
@@ -201,18 +170,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         const int bt = tlin / g.tiles_per_batch;
         const int t = tlin - bt * g.tiles_per_batch;
         int tm, tn;
-        if constexpr (!Tr::kSymmetric) {
-            // Grouped order: runs of group_n column tiles, walked row by row, so the
-            // tiles an XCD holds at once share few row- and column-operand panels.
-            const int gn = g.group_n;
-            const int span = gn * g.tiles_m;
-            const int grp = t / span, r = t - grp * span;
-            const int width = min(gn, g.tiles_n - grp * gn);
-            tm = r / width;
-            tn = grp * gn + r % width;
-        } else {
-            upper_tile_blocked(t, g.tiles_m, g.group_n, tm, tn);
-        }
+        tile_coords(g, Tr::kSymmetric, t, tm, tn);
         const int row0 = tm * BM, col0 = tn * BN;
 
         const i32x4 rs_row = make_buffer_rsrc(g.rowop + bt * g.sb_row, g.bytes_row);
@@ -612,7 +570,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
             const __amdgpu_buffer_rsrc_t rs_part =
                 __builtin_amdgcn_make_buffer_rsrc(g.partials, 0, 0x7fffffff, 0x00020000);
             auto lane_base = [&](int u) {
-                return static_cast<uint32_t>(int64_t(sk_slot(g, u, lt)) * slot_bytes) + tid * 16;
+                return static_cast<uint32_t>(int64_t(sk_slot(u, lt)) * slot_bytes) + tid * 16;
             };
             // Slot layout: 16-byte chunk c = (i * SN + j) * 4 + q of every thread,
             // thread-minor, so each access instruction covers 1 KiB contiguously.

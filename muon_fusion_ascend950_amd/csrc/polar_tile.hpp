@@ -188,54 +188,6 @@ __device__ __forceinline__ bf16x8 frag_nc_tr(const uint16_t *lds, int n0, int kk
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// Output tile (tm, tn) of linear tile index t within one batch matrix for the
-// triangular stages: row-major walk over the upper tiles tn >= tm of an nt x nt grid.
-__device__ __forceinline__ void upper_tile_of(int t, int nt, int &tm, int &tn) {
-    int row = 0, len = nt;
-    while (t >= len) {
-        t -= len;
-        ++row;
-        --len;
-    }
-    tm = row;
-    tn = row + t;
-}
-
-// The same tiles walked in B x B super-blocks: super-blocks (I, J >= I) row-major,
-// the tiles of each row-major inside it (tn >= tm in a diagonal one).  A run of
-// consecutive tiles then covers a compact block of the triangle, whose row and
-// column panels (blocks of X rows for gram, of A rows for poly) are few and shared
-// in one XCD's L2.  B <= 1: the row-major walk.
-__device__ __forceinline__ void upper_tile_blocked(int t, int nt, int b, int &tm, int &tn) {
-    if (b <= 1) {
-        upper_tile_of(t, nt, tm, tn);
-        return;
-    }
-    const int ns = (nt + b - 1) / b;
-    tm = tn = 0;
-    for (int bi = 0; bi < ns; ++bi) {
-        const int rows = min(b, nt - bi * b);
-        const int diag = rows * (rows + 1) / 2;
-        if (t < diag) {
-            int r, c;
-            upper_tile_of(t, rows, r, c);
-            tm = bi * b + r;
-            tn = bi * b + c;
-            return;
-        }
-        t -= diag;
-        for (int bj = bi + 1; bj < ns; ++bj) {
-            const int cols = min(b, nt - bj * b);
-            if (t < rows * cols) {
-                tm = bi * b + t / cols;
-                tn = bj * b + t % cols;
-                return;
-            }
-            t -= rows * cols;
-        }
-    }
-}
-
 __device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }

@@ -362,3 +362,24 @@ def test_build_entry_does_not_import_the_package():
     root = Path(__file__).resolve().parents[1]
     r = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_in_place_step_and_apply_are_rejected():
+    """y over x would race (every apply tile reads X's whole K range while other
+    tiles write Y): the step and the apply stage refuse it before any launch."""
+    lib = capi.load()
+    info = capi.query(1, 64, 128)
+    x = 1 << 20  # never dereferenced: the checks fail first
+    ws = 1 << 32
+    st = lib.muon_polar_step(x, x, ws, info.workspace_bytes, 1, 64, 128, 1.0, 1.0, 1.0, None)
+    assert st == capi.ERR_INVALID_ARGUMENT and "must not overlap" in capi.last_error()
+    st = lib.muon_polar_step(x, x + 64 * 128, ws, info.workspace_bytes, 1, 64, 128, 1.0, 1.0,
+                             1.0, None)  # half-overlapping rows
+    assert st == capi.ERR_INVALID_ARGUMENT and "must not overlap" in capi.last_error()
+    st = lib.muon_polar_step(x, ws + 4096, ws, info.workspace_bytes, 1, 64, 128, 1.0, 1.0, 1.0,
+                             None)  # y inside the workspace
+    assert st == capi.ERR_INVALID_ARGUMENT and "workspace must not overlap" in capi.last_error()
+    st = lib.muon_polar_apply(ws, x, x, None, 0, 1, 64, 128, 1.0, None)
+    assert st == capi.ERR_INVALID_ARGUMENT and "must not overlap" in capi.last_error()
+    st = lib.muon_polar_apply(ws, x, ws + 256, None, 0, 1, 64, 128, 1.0, None)
+    assert st == capi.ERR_INVALID_ARGUMENT and "poly and y must not overlap" in capi.last_error()

@@ -1,0 +1,105 @@
+"""Every store the stage kernels can make stays inside its buffer (CPU only).
+
+``muon_polar_check_plan`` builds the launch plan ``muon_polar_step`` would use on a
+device of 256 CUs and walks every workgroup of each stage with the kernels' own
+schedule functions (``csrc/polar_schedule.hpp``): the output tiles and mirrored
+tiles it stores, the stream-K partial slots it writes or reads and its arrival
+word.  These tests assert that each range lies inside the buffer it belongs to, that
+the (tile, K-step) iterations are computed exactly once, and that the operands'
+per-matrix byte extents fit the kernels' 32-bit buffer offsets.
+
+The occupancy (resident workgroups per CU) decides the stream-K split; it is swept
+over 1-4 per stage, which covers what the device reports for every kernel.
+"""
+
+from __future__ import annotations
+
+import pytest
+
+from muon_fusion_ascend950_amd import capi
+
+BASELINE_SHAPES = [(4, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (8, 512, 2048),
+                   (2, 150, 2050), (1, 129, 130)]
+MORE_SHAPES = [(3, 1024, 4096), (16, 256, 1024), (1, 1000, 3000), (2, 700, 1800), (1, 3000, 1000),
+               (1, 8192, 16384), (2, 6144, 8192), (4000, 16, 40), (1, 64, 100000), (1, 2048, 520)]
+OCCUPANCIES = [(1, 1, 1), (2, 2, 2), (1, 2, 2), (2, 1, 1), (3, 3, 3), (4, 4, 4)]
+
+
+def check(plan: capi.PlanExtents) -> None:
+    assert plan.poly_offset >= plan.gram_bytes
+    assert plan.counters_offset >= plan.poly_offset + plan.gram_bytes
+    assert plan.partials_offset >= plan.counters_offset + 3 * plan.counter_stride * 8
+    assert plan.pad_offset >= plan.partials_offset
+    assert plan.pad_end <= plan.workspace_bytes
+    for s in range(3):
+        e = plan.stage[s]
+        assert e.coverage_ok == 1, f"stage {s}: an iteration is not computed exactly once"
+        assert e.extents_ok == 1, f"stage {s}: an operand extent does not fit 32-bit offsets"
+        assert 0 <= e.out_lo <= e.out_hi <= e.out_limit, (
+            f"stage {s}: stores [{e.out_lo}, {e.out_hi}) outside an output of {e.out_limit} bytes")
+        if e.sk_units > 0:
+            assert e.dma_fed == 1
+            assert 0 <= e.partial_lo < e.partial_hi <= e.partial_limit, (
+                f"stage {s}: partial slots [{e.partial_lo}, {e.partial_hi}) outside "
+                f"{e.partial_limit} bytes")
+            assert 0 < e.counter_hi <= e.counter_limit
+            # partial offsets are 32-bit in the kernel
+            assert e.partial_hi < 2**31
+        else:
+            assert e.partial_hi == 0 and e.counter_hi == 0
+
+
+@pytest.mark.parametrize("occ", OCCUPANCIES)
+@pytest.mark.parametrize("shape", BASELINE_SHAPES)
+def test_baseline_plans_store_inside_their_buffers(shape, occ):
+    check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
+
+
+@pytest.mark.parametrize("occ", [(1, 1, 1), (2, 2, 2)])
+@pytest.mark.parametrize("shape", MORE_SHAPES)
+def test_other_plans_store_inside_their_buffers(shape, occ):
+    check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
+
+
+def test_headline_plan_splits_every_stage():
+    """The walk covers the stream-K path: at [4096,14336] with one 256x256
+    workgroup per CU every stage cuts its last round."""
+    plan = capi.check_plan(1, 4096, 14336, cus=256, blocks_per_cu=(1, 1, 1))
+    for s in range(3):
+        e = plan.stage[s]
+        assert (e.tile_m, e.tile_n, e.waves) == (256, 256, 8)
+        assert e.sk_units > 0 and e.dp_tiles < e.total_tiles
+    # gram: 136 upper tiles, all in the split; apply: 896 tiles, 3 whole rounds
+    assert plan.stage[0].total_tiles == 136 and plan.stage[0].dp_tiles == 0
+    assert plan.stage[2].total_tiles == 896 and plan.stage[2].dp_tiles == 768
+
+
+@pytest.mark.parametrize("env", [{"MUON_POLAR_WAVES": "4"},
+                                 {"MUON_POLAR_GRAM_TILE": "128", "MUON_POLAR_POLY_TILE": "128"},
+                                 {"MUON_POLAR_GRAM_TILE": "192", "MUON_POLAR_POLY_TILE": "192"},
+                                 {"MUON_POLAR_APPLY_TILE_M": "128", "MUON_POLAR_APPLY_TILE_N": "256"},
+                                 {"MUON_POLAR_APPLY_TILE_M": "256", "MUON_POLAR_APPLY_TILE_N": "128"},
+                                 {"MUON_POLAR_SYM_GROUP": "1"}, {"MUON_POLAR_APPLY_GROUP_N": "3"},
+                                 {"MUON_POLAR_STREAM": "0"}])
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (2, 700, 1800), (8, 512, 2048)])
+def test_tuned_plans_store_inside_their_buffers(monkeypatch, env, shape):
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    for occ in [(1, 1, 1), (2, 2, 2)]:
+        check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
+
+
+def test_without_a_device_count_nothing_splits():
+    plan = capi.check_plan(1, 4096, 14336, cus=0, blocks_per_cu=(1, 1, 1))
+    check(plan)
+    assert all(plan.stage[s].sk_units == 0 for s in range(3))
+
+
+@pytest.mark.parametrize("shape", [(1, 32512, 33025), (1, 10_000_000, 72), (1, 20_000_000, 8)])
+def test_padded_copy_beyond_32_bit_offsets_is_rejected(shape):
+    """X fits 32-bit offsets but its copy padded to a multiple of 64 columns would
+    not (2.15-2.56 GB): the out-of-range marker of the DMA (offset 2^31) would then
+    address real rows.  Such shapes are rejected."""
+    with pytest.raises(capi.CapiError, match="too large") as err:
+        capi.query(*shape)
+    assert err.value.status == capi.ERR_INVALID_ARGUMENT

@@ -338,6 +338,25 @@ def test_batch_equals_per_matrix_and_is_deterministic():
     assert torch.equal(y, polar_step(x, *C0))
 
 
+@pytest.mark.parametrize("shape", [(1, 512, 8192), (2, 256, 4096), (8, 512, 2048)])
+def test_misaligned_contiguous_input_takes_the_aligned_route(shape):
+    """A contiguous X at an odd address (buf[1:].view(...)): the op copies it to an
+    aligned buffer, so it runs the DMA-fed kernels and their stream-K split like an
+    aligned input, bit for bit (the register-staged kernels would sum the split
+    shapes' K terms in another order)."""
+    b, m, n = shape
+    x = O.make_input(shape, seed=12).to(DEV)
+    buf = torch.empty(b * m * n + 1, dtype=torch.bfloat16, device=DEV)
+    buf[1:].copy_(x.reshape(-1))
+    xm = buf[1:].view(b, m, n)
+    assert xm.is_contiguous() and xm.data_ptr() % 16 != 0
+    assert torch.equal(polar_step(xm, *C0), polar_step(x, *C0))
+    from muon_fusion_ascend950_amd import polar_express
+
+    assert torch.equal(polar_express(xm, O.COEFFICIENTS[:2]), polar_express(x, O.COEFFICIENTS[:2]))
+    assert torch.equal(xm, x)  # the input is read only
+
+
 def test_noncontiguous_input():
     base = O.make_input((2, 300, 200), seed=10).to(DEV)
     x = base.transpose(1, 2)  # [2, 200, 300] non-contiguous
@@ -494,8 +513,13 @@ def _fp32_formula(x: torch.Tensor, coefficients) -> torch.Tensor:
 
 @pytest.mark.parametrize("shape,steps", [((8, 512, 2048), 1), ((8, 512, 2048), 5),
                                          ((4096, 14336), 1), ((14336, 4096), 1),
-                                         ((4, 4096, 4096), 1), ((4096, 14336), 5)])
+                                         ((4, 4096, 4096), 1), ((4096, 14336), 5),
+                                         ((4, 4096, 4096), 5), ((14336, 4096), 5)])
 def test_baseline_shapes(shape, steps):
+    """Every BASELINE.json workload on its default route (stream-K split on: the large
+    shapes cut their last round), against the fp32 formula with the reference's 6e-2
+    gate (tests/test_polar_step.py:42,53) and the normwise bound."""
+    print(f"baseline {shape} x{steps}", flush=True)
     x = O.make_input(shape, seed=0).to(DEV)
     coeffs = O.COEFFICIENTS[:steps]
     y = x
