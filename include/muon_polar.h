@@ -99,6 +99,19 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
                     int64_t batch, int64_t m, int64_t n,
                     double a, double b, double c, hipStream_t stream);
 
+/* muon_polar_step without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No reference counterpart.
+ * The workspace is a device array of 192 MiB (201326592 bytes) inside the
+ * library, one per GPU, held from the first call on that GPU until the process
+ * ends; shapes whose workspace (info.workspace_bytes) is larger are rejected
+ * with MUON_POLAR_ERR_WORKSPACE (e.g. [4, 4096, 4096]; [4096, 14336] fits).
+ * Results equal muon_polar_step's bit for bit.  No device memory is allocated
+ * and no caller buffer is needed beyond x and y.  Calls that overlap on one GPU
+ * (other streams, other threads) share the array and race: serialise them. */
+int muon_polar_step_noalloc(const void *x, void *y, int64_t batch, int64_t m, int64_t n,
+                            double a, double b, double c, hipStream_t stream);
+
 /* The three stages one at a time.  `workspace` is NULL (workspace_bytes
  * ignored: the stage runs one output tile per workgroup) or a buffer of
  * info.workspace_bytes, the same one muon_polar_step takes (gram / poly may be

@@ -74,7 +74,8 @@ def _torch_paths() -> tuple[list[str], Path]:
 def build_hip_library(verbose: bool = True) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     common = HIP_FLAGS + [f"-I{INCLUDE}", f"-I{CSRC}"]
-    sources = ["polar_kernels.hip", "polar_stream.hip", "polar_norm.hip", "polar_capi.cpp"]
+    sources = ["polar_kernels.hip", "polar_stream.hip", "polar_norm.hip", "polar_noalloc.hip",
+               "polar_capi.cpp"]
     objects = [BUILD_DIR / (Path(src).stem + ".o") for src in sources]
     jobs = [[_hipcc(), "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)] + common
             for src, obj in zip(sources, objects)]

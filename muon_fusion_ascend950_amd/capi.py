@@ -15,6 +15,7 @@ from pathlib import Path
 EXPORTED_FUNCTIONS = (
     "muon_polar_query",
     "muon_polar_step",
+    "muon_polar_step_noalloc",
     "muon_polar_gram",
     "muon_polar_poly",
     "muon_polar_apply",
@@ -89,6 +90,7 @@ def load() -> ctypes.CDLL:
     i64, vp, sz, dbl = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_double
     lib.muon_polar_query.argtypes = [i64, i64, i64, ctypes.POINTER(ShapeInfo)]
     lib.muon_polar_step.argtypes = [vp, vp, vp, sz, i64, i64, i64, dbl, dbl, dbl, vp]
+    lib.muon_polar_step_noalloc.argtypes = [vp, vp, i64, i64, i64, dbl, dbl, dbl, vp]
     lib.muon_polar_gram.argtypes = [vp, vp, vp, sz, i64, i64, i64, vp]
     lib.muon_polar_poly.argtypes = [vp, vp, vp, sz, i64, i64, i64, dbl, dbl, vp]
     lib.muon_polar_apply.argtypes = [vp, vp, vp, vp, sz, i64, i64, i64, dbl, vp]
@@ -99,7 +101,8 @@ def load() -> ctypes.CDLL:
                                            vp]
     lib.muon_polar_check_plan.argtypes = [i64, i64, i64, ctypes.c_int,
                                           ctypes.POINTER(ctypes.c_int), ctypes.POINTER(PlanExtents)]
-    for name in ("muon_polar_query", "muon_polar_step", "muon_polar_gram", "muon_polar_poly",
+    for name in ("muon_polar_query", "muon_polar_step", "muon_polar_step_noalloc",
+                 "muon_polar_gram", "muon_polar_poly",
                  "muon_polar_apply", "muon_polar_express", "muon_polar_muon_update",
                  "muon_polar_check_plan"):
         getattr(lib, name).restype = ctypes.c_int
@@ -163,6 +166,13 @@ def step(x, y, workspace, a: float, b: float, c: float, stream=None) -> None:
     check("muon_polar_step", load().muon_polar_step(
         x.data_ptr(), y.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
         batch, m, n, float(a), float(b), float(c), _stream(stream)))
+
+
+def step_noalloc(x, y, a: float, b: float, c: float, stream=None) -> None:
+    """muon_polar_step_noalloc: the step with the library's own per-GPU scratch."""
+    batch, m, n = _bmn(x)
+    check("muon_polar_step_noalloc", load().muon_polar_step_noalloc(
+        x.data_ptr(), y.data_ptr(), batch, m, n, float(a), float(b), float(c), _stream(stream)))
 
 
 def _ws(workspace):

@@ -1071,6 +1071,38 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
     return run_step(p, x, y, workspace, batch, a, b, c, stream);
 }
 
+int muon_polar_step_noalloc(const void *x, void *y, int64_t batch, int64_t m, int64_t n,
+                            double a, double b, double c, hipStream_t stream) {
+    if (x == nullptr || y == nullptr)
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "null pointer");
+    Plan p{};
+    int st = get_plan(batch, m, n, p);
+    if (st != MUON_POLAR_OK) return st;
+    if (p.workspace_bytes > muon_polar::kNoAllocScratchBytes)
+        return fail(MUON_POLAR_ERR_WORKSPACE,
+                    "this shape needs " + std::to_string(p.workspace_bytes) +
+                        " bytes of scratch; muon_polar_step_noalloc holds " +
+                        std::to_string(muon_polar::kNoAllocScratchBytes) +
+                        " per device (call muon_polar_step with a workspace)");
+    if (p.tall) {
+        st = check_tall(p, x, y);
+        if (st != MUON_POLAR_OK) return st;
+    }
+    const size_t xy_bytes = static_cast<size_t>(batch * m * n * 2);
+    if (overlaps(x, xy_bytes, y, xy_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "x and y must not overlap");
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess)
+        return fail(MUON_POLAR_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    void *scratch = nullptr;
+    e = muon_polar::noalloc_scratch(device, &scratch);
+    if (e != hipSuccess)
+        return fail(MUON_POLAR_ERR_HIP,
+                    std::string("scratch address (hipGetSymbolAddress): ") + hipGetErrorString(e));
+    return run_step(p, x, y, scratch, batch, a, b, c, stream);
+}
+
 int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace_bytes,
                        int64_t batch, int64_t m, int64_t n, const double *coefficients,
                        int64_t steps, int normalize, hipStream_t stream) {

@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime_api.h>
+#include <cstddef>
 #include <cstdint>
 
 namespace muon_polar {
@@ -62,7 +63,8 @@ struct GemmArgs {
     int32_t dp_tiles;               // == total_tiles when stream-K is off
     int32_t sk_units;               // 0 or a multiple of 8
     int64_t sk_iters;
-    float *partials;                // 2 * sk_units slots of BM * BN floats
+    float *partials;                // sk_units + (total_tiles - dp_tiles) - 1 slots of
+                                    // BM * BN floats (sk_slot, polar_schedule.hpp)
     // One arrival word per stream-K tile: (token << 32) | count.  A word holding
     // another launch's token counts as zero, so the words need no clearing; the
     // last contributor leaves (token << 32) | 0, which a replay of the same
@@ -122,5 +124,11 @@ hipError_t launch_pad_rows(const uint16_t *x, uint16_t *xp, int64_t rows, int64_
 // p ← p·decay + alpha·O over `total` elements; vec: total % 8 == 0, 16-byte aligned.
 hipError_t launch_muon_param_update(float *p, const uint16_t *o, int64_t total, float decay,
                                     float alpha, bool vec, hipStream_t stream);
+
+// Scratch of the allocation-free step (polar_noalloc.hip): a device array of
+// kNoAllocScratchBytes per GPU.  noalloc_scratch returns its address on
+// `device`, which must be the current device (looked up once per device).
+constexpr size_t kNoAllocScratchBytes = size_t(192) << 20;
+hipError_t noalloc_scratch(int device, void **ptr);
 
 }  // namespace muon_polar
