@@ -6,12 +6,25 @@ single ``polar_step`` on a bf16 [4096,14336] matrix with inputs resident in HBM,
 counting the credited FLOPs M²N + 2M³ + 2M²N per matrix.  The [8,512,2048] case is
 reported in ``secondary``.
 
-Timing follows the driver contract (W untimed warm-up calls, then exactly K calls
-between two device synchronisations) — the reference's own method is the same loop
-(README.md:179-191).  Per-kernel durations come from HIP events recorded on the
-launch stream between the stages of a step sequence launched through the C ABI (so each
-stage sees the caches as inside a step); ``roofline`` uses the dominant kernel (stage 3,
-P·X + a·X).
+Order of a run (rank 0, one GPU):
+
+1. accuracy gate of the headline input (the reference's method runs its
+   ``assert_close(…, 6e-2)`` before timing, README.md:179-203), then ``--settle-s``
+   seconds of headline calls: from idle the GPU's power management needs about 50
+   steps (≈35 ms of load) to reach its steady clock — the first 2 steps run fast, steps
+   3-5 at ~1.4x their steady time, then the clock recovers — so a short W/K window
+   would otherwise time that transient;
+2. the driver contract: W untimed warm-up calls, then exactly K timed calls between two
+   device synchronisations → ``value``, ``ms_per_step``;
+3. per-stage device times (``kernel_us``): R back-to-back launches of one stage through
+   the C ABI, captured in a HIP graph and replayed between two HIP events on the launch
+   stream (no host gaps, no event fences between stages), with the step's workspace and
+   stream-K split; ``roofline`` uses stage 3 (P·X + a·X), the dominant kernel;
+4. every BASELINE.json configuration with the reference's timing method (20 warm-ups,
+   then the median of 5 repeats of 100 calls, README.md:179-191) after its accuracy gate
+   (6e-2 against the fp32 formula, and relF = ‖Y − Y_fp32‖_F / ‖Y_fp32‖_F);
+5. comparison points (PyTorch eager on the GPU, five steps, the Muon update) and the
+   CPU baseline (the oracle's restatement of the reference formula on the host cores).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -21,6 +34,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import re
 import statistics
 import sys
@@ -36,6 +50,7 @@ PEAK_HBM_GBS = 8000.0
 COEFFS = (8.156554524902461, -22.48329292557795, 15.878769915207462)  # tests/test_polar_step.py:14
 HEADLINE = (1, 4096, 14336)
 SECONDARY = (8, 512, 2048)
+GATE_TOL = 6e-2  # tests/test_polar_step.py:42,53
 # Every BASELINE.json configuration on the GPU: (config, shape, steps per call).  Config 0 is
 # the reference's CPU plumbing case, timed here on the GPU as well; five-step calls chain the
 # five coefficient triples (polar_express without normalisation = five polar_step calls).
@@ -51,41 +66,14 @@ CONFIGS = (
     ("cfg4", (4, 4096, 4096), 1),
     ("cfg4", (4, 4096, 4096), 5),
 )
+# CPU baseline shapes: shape and runs after one warm-up
+CPU_SHAPES = (((129, 130), 5), ((2, 150, 2050), 5), ((8, 512, 2048), 5), ((4096, 14336), 3),
+              ((4, 4096, 4096), 3))
 TRAFFIC_SUMMARY = ROOT / "profiles" / "apply_4096x14336_hbm_traffic.txt"
+STAGES = ("gram", "poly", "apply")
 
 
-def config_call(shape, steps: int):
-    """The GPU call of one configuration: one polar_step, or the five-step chain."""
-    import torch
-    import muon_fusion_ascend950_amd as mf
-
-    x = make_input(shape, seed=0).cuda()
-    if steps == 1:
-        a, b, c = COEFFS
-        return (lambda: mf.polar_step(x, a, b, c)), x
-    coeffs = mf.COEFFICIENTS[:steps]
-    return (lambda: mf.polar_express(x, coeffs, normalize=False)), x
-
-
-def all_configs(calls_budget_s: float = 0.25):
-    """µs per call and credited TFLOP/s (% of the dense bf16 peak) of every configuration."""
-    rows = []
-    for name, shape, steps in CONFIGS:
-        fn, x = config_call(shape, steps)
-        batch = shape[0] if len(shape) == 3 else 1
-        m, n = shape[-2], shape[-1]
-        once = time_calls(fn, 3, 2)
-        calls = max(5, min(200, int(calls_budget_s / max(once, 1e-6))))
-        sec = time_calls(fn, calls, 3)
-        flops = steps * credited_flops(batch, m, n)
-        rows.append({"config": name, "shape": list(shape), "steps_per_call": steps,
-                     "us_per_call": round(sec * 1e6, 2),
-                     "tflops": round(flops / sec / 1e12, 2),
-                     "pct_bf16_peak": round(100 * flops / sec / 1e12 / PEAK_BF16_TFLOPS, 2)})
-        del x
-    return rows
-
-
+# ----------------------------------------------------------------------------- workloads
 def credited_flops(batch: int, m: int, n: int) -> int:
     m, n = min(m, n), max(m, n)
     return batch * (m * m * n + 2 * m**3 + 2 * m * m * n)
@@ -100,6 +88,52 @@ def make_input(shape, seed: int = 0):
     return x / (x.norm(dim=(-2, -1), keepdim=True) * 1.01 + 1e-6)
 
 
+def torch_formula(x, coefficients):
+    """The reference's formula (tests/test_polar_step.py:22-28, README.md:172-174) in
+    plain PyTorch at x's dtype: gram = x @ x.mT; x = a*x + (b*gram + c*gram@gram) @ x.
+    The transposed operand is materialised first (batched bf16 products with a transposed
+    right operand are avoided on ROCm)."""
+    import torch
+
+    out = x
+    for a, b, c in coefficients:
+        gram = torch.matmul(out, out.mT.contiguous())
+        out = a * out + torch.matmul(b * gram + c * torch.matmul(gram, gram), out)
+    return out
+
+
+def config_call(shape, steps: int):
+    """The GPU call of one configuration: one polar_step, or the five-step chain."""
+    import muon_fusion_ascend950_amd as mf
+
+    x = make_input(shape, seed=0).cuda()
+    if steps == 1:
+        a, b, c = COEFFS
+        return (lambda: mf.polar_step(x, a, b, c)), x
+    coeffs = mf.COEFFICIENTS[:steps]
+    return (lambda: mf.polar_express(x, coeffs, normalize=False)), x
+
+
+def accuracy(y, x, coefficients) -> dict:
+    """The reference's gate (assert_close rtol = atol = 6e-2 against the formula, here in
+    fp32 on the GPU) and the normwise error relF, which the gate alone cannot replace (an
+    all-zero output passes it at these magnitudes)."""
+    import torch
+
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        ref = torch_formula(x.float(), coefficients)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+    yf = y.float()
+    ok = bool(torch.isclose(yf, ref, rtol=GATE_TOL, atol=GATE_TOL).all().item())
+    rel = ((yf - ref).norm() / ref.norm()).item()
+    del ref, yf
+    return {"gate_6e-2": "pass" if ok else "FAIL", "relF_vs_fp32_formula": float(f"{rel:.3e}")}
+
+
+# ----------------------------------------------------------------------------- timing
 def time_calls(fn, steps: int, warmup: int) -> float:
     """Seconds per call: warm-up, then exactly `steps` calls between synchronisations."""
     import torch
@@ -114,29 +148,43 @@ def time_calls(fn, steps: int, warmup: int) -> float:
     return (time.perf_counter() - t0) / steps
 
 
-def kernel_us(fn, launches: int, warmup: int = 3) -> float:
-    """Average device duration (µs) of one launch, from HIP events on the current stream."""
+def reference_method(fn, warmup: int = 20, calls: int = 100, repeats: int = 5) -> float:
+    """README.md:179-191: warm-up, then the median over `repeats` of `calls` back-to-back
+    calls bracketed by device synchronisations (seconds per call)."""
     import torch
 
     for _ in range(warmup):
         fn()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    start.record()
-    for _ in range(launches):
-        fn()
-    stop.record()
-    stop.synchronize()
-    return start.elapsed_time(stop) * 1e3 / launches
+    samples = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        torch.cuda.synchronize()
+        samples.append((time.perf_counter() - t0) / calls)
+    return statistics.median(samples)
 
 
-def stage_times(batch: int, m: int, n: int, launches: int, warmup: int = 3):
-    """µs per launch of each stage as it runs inside a step: gram, poly and apply are
-    launched in step order through the C ABI with polar_step's workspace (A and P in
-    it, the same stream-K split as in the step), `launches` times, with HIP events on
-    torch's current stream (the launch stream) between the stages; each stage's time is
-    the sum of its event intervals / launches."""
+def settle(fn, seconds: float) -> int:
+    """Run `fn` back to back for `seconds` (the GPU's clock settles under sustained load)."""
+    import torch
+
+    calls = 0
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            fn()
+        calls += 10
+        torch.cuda.synchronize()
+    return calls
+
+
+def stage_times(batch: int, m: int, n: int, launches: int, repeats: int = 3) -> dict:
+    """µs per launch of each stage: `launches` back-to-back launches of one stage through
+    the C ABI (polar_step's workspace, A and P in it, the same stream-K split as inside
+    the step), captured in a HIP graph and replayed between two HIP events on the
+    capturing stream, the stream the kernels run on; the median of `repeats` replays."""
     import torch
     from muon_fusion_ascend950_amd import capi
 
@@ -148,36 +196,39 @@ def stage_times(batch: int, m: int, n: int, launches: int, warmup: int = 3):
     poly = ws[p_off:p_off + info.gram_bytes].view(torch.bfloat16).view(batch, mp, mp)
     y = torch.empty_like(x)
     a, b, c = COEFFS
-    stages = (("gram", lambda: capi.gram(x, gram, workspace=ws)),
-              ("poly", lambda: capi.poly(gram, poly, batch, m, n, b, c, workspace=ws)),
-              ("apply", lambda: capi.apply(poly, x, y, a, workspace=ws)))
-    for _ in range(warmup):
-        for _, fn in stages:
-            fn()
+    calls = {"gram": lambda: capi.gram(x, gram, workspace=ws),
+             "poly": lambda: capi.poly(gram, poly, batch, m, n, b, c, workspace=ws),
+             "apply": lambda: capi.apply(poly, x, y, a, workspace=ws)}
+    for name in STAGES:  # A and P in place before any stage is timed
+        calls[name]()
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
-              for _ in range(launches)]
-    for ev in events:
-        ev[0].record()
-        for i, (_, fn) in enumerate(stages):
-            fn()
-            ev[i + 1].record()
+    out = {}
+    stream = torch.cuda.Stream()
+    for name in STAGES:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for _ in range(launches):
+                    calls[name]()
+        graph.replay()  # warm-up replay
+        torch.cuda.synchronize()
+        samples = []
+        for _ in range(repeats):
+            start = torch.cuda.Event(enable_timing=True)
+            stop = torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                start.record()
+                graph.replay()
+                stop.record()
+            stop.synchronize()
+            samples.append(start.elapsed_time(stop) * 1e3 / launches)
+        out[name] = statistics.median(samples)
+        del graph
     torch.cuda.synchronize()
-    return {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in events) * 1e3 / launches
-            for i, (name, _) in enumerate(stages)}
+    return out
 
 
-def torch_eager(x):
-    """The README's comparison point (README.md:172-174), plain PyTorch on the GPU.
-    The transposed operand is materialised first (batched bf16 products with a
-    transposed right operand are avoided on ROCm)."""
-    import torch
-
-    a, b, c = COEFFS
-    gram = torch.matmul(x, x.mT.contiguous())
-    return a * x + torch.matmul(b * gram + c * torch.matmul(gram, gram), x)
-
-
+# ----------------------------------------------------------------------------- comparison points
 MUON_LR, MUON_MOMENTUM, MUON_WD = 0.02, 0.95, 0.01
 
 
@@ -196,15 +247,11 @@ def muon_eager_step(p, g, buf, coefficients):
     """nanochat's Muon step in plain PyTorch on the GPU (momentum lerps, bf16 Polar
     Express with the reference recipe's normalisation, decoupled decay, shape-scaled
     add): the comparison point of the native update."""
-    import torch
-
     buf.lerp_(g, 1 - MUON_MOMENTUM)
     u = g.lerp(buf, MUON_MOMENTUM)
     x = u.bfloat16()
     x = x / (x.norm(dim=(-2, -1), keepdim=True) * 1.01 + 1e-6)
-    for a, b, c in coefficients:
-        gram = torch.matmul(x, x.mT.contiguous())
-        x = a * x + torch.matmul(b * gram + c * torch.matmul(gram, gram), x)
+    x = torch_formula(x, coefficients)
     p.mul_(1 - MUON_LR * MUON_WD)
     p.add_(x, alpha=-MUON_LR * max(1.0, p.size(-2) / p.size(-1)) ** 0.5)
 
@@ -217,34 +264,126 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(budget_s: float = 12.0):
-    """The oracle's restatement of the reference formula, bf16 torch on the host CPU."""
+def run_metadata() -> dict:
+    """What the reference asks results to be published with (README.md:208): device,
+    framework versions, tuning variables and the timing method."""
+    import torch
+
+    props = torch.cuda.get_device_properties(0)
+    tuning = {k: v for k, v in sorted(os.environ.items()) if k.startswith("MUON_POLAR_")}
+    return {
+        "device": props.name,
+        "arch": getattr(props, "gcnArchName", ""),
+        "compute_units": props.multi_processor_count,
+        "torch": torch.__version__,
+        "hip": torch.version.hip,
+        "python": platform.python_version(),
+        "tuning_variables": tuning or "defaults",
+        "timing": ("value: settle, W warm-up calls, K calls between device synchronisations; "
+                   "all_configs: 20 warm-ups, median of 5 x 100 calls (README.md:179-191); "
+                   "kernel_us: back-to-back launches of one stage, HIP-graph replay between "
+                   "HIP events on the launch stream"),
+    }
+
+
+def cpu_info() -> dict:
+    model, flags = "", set()
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name") and not model:
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    isa = [f for f in ("amx_bf16", "amx_tile", "avx512_bf16", "avx512f", "avx2") if f in flags]
+    return {"cpu_model": model, "isa_flags": isa}
+
+
+def cpu_baseline() -> dict:
+    """The oracle's restatement of the reference formula, bf16 torch on the host CPU.
+
+    Threads: the host cores this process may use (its affinity), capped at the box's CPU
+    share of 16 threads per GPU (the GPU boxes give each GPU 16 host threads and set
+    OMP_NUM_THREADS to that)."""
     import torch
     from oracle import polar_oracle as O
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    cores = max(1, min(affinity, share))
     torch.set_num_threads(cores)
-    batch, m, n = HEADLINE
-    x = make_input((m, n), seed=0)
-    samples = []
+    rows = []
+    headline = None
     with torch.no_grad():
-        O.reference_formula_torch(x, [COEFFS])  # warm-up
-        t_end = time.perf_counter() + budget_s
-        while len(samples) < 3 or (time.perf_counter() < t_end and len(samples) < 15):
-            t0 = time.perf_counter()
-            O.reference_formula_torch(x, [COEFFS])
-            samples.append(time.perf_counter() - t0)
-    med = statistics.median(samples)
-    flops = credited_flops(batch, m, n)
+        for shape, runs in CPU_SHAPES:
+            x = make_input(shape, seed=0)
+            O.reference_formula_torch(x, [COEFFS])  # warm-up
+            samples = []
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                O.reference_formula_torch(x, [COEFFS])
+                samples.append(time.perf_counter() - t0)
+            med = statistics.median(samples)
+            batch = shape[0] if len(shape) == 3 else 1
+            tf = credited_flops(batch, shape[-2], shape[-1]) / med / 1e12
+            rows.append({"shape": list(shape), "runs": runs, "us_per_step": round(med * 1e6, 1),
+                         "tflops": round(tf, 4)})
+            if tuple(shape) == HEADLINE[1:]:
+                headline = (tf, med, runs)
+    tf, med, runs = headline
     return {
-        "value": round(flops / med / 1e12, 4),
+        "value": round(tf, 4),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"reference formula (tests/test_polar_step.py:22-28) in bf16 torch on the host CPU, "
-                   f"[4096,14336] one step, median of {len(samples)} runs after 1 warm-up "
-                   f"({med * 1e3:.0f} ms/step)"),
+        "sample": (f"reference formula (tests/test_polar_step.py:22-28) in bf16 torch on the host "
+                   f"CPU, [4096,14336] one step, median of {runs} runs after 1 warm-up "
+                   f"({med * 1e3:.0f} ms/step); other BASELINE shapes in 'shapes'"),
+        "torch_threads": torch.get_num_threads(),
+        "affinity_cores": affinity,
+        **cpu_info(),
+        "shapes": rows,
     }
+
+
+# ----------------------------------------------------------------------------- phases
+def all_configs():
+    """µs per call (reference method), credited TFLOP/s, % of the dense bf16 peak and the
+    accuracy gate of every BASELINE.json configuration."""
+    rows = []
+    for name, shape, steps in CONFIGS:
+        import muon_fusion_ascend950_amd as mf
+
+        fn, x = config_call(shape, steps)
+        gate = accuracy(fn(), x, mf.COEFFICIENTS[:steps] if steps > 1 else [COEFFS])
+        batch = shape[0] if len(shape) == 3 else 1
+        m, n = shape[-2], shape[-1]
+        sec = reference_method(fn)
+        flops = steps * credited_flops(batch, m, n)
+        rows.append({"config": name, "shape": list(shape), "steps_per_call": steps,
+                     "us_per_call": round(sec * 1e6, 2),
+                     "tflops": round(flops / sec / 1e12, 2),
+                     "pct_bf16_peak": round(100 * flops / sec / 1e12 / PEAK_BF16_TFLOPS, 2),
+                     **gate})
+        print(json.dumps({"config": name, "shape": list(shape), "steps": steps,
+                          "us_per_call": round(sec * 1e6, 2), **gate}), file=sys.stderr, flush=True)
+        del x
+    return rows
+
+
+def headline_phase(args, x):
+    """Gate, settle, then the contract's W + K calls; per-stage times after it."""
+    import torch
+    import muon_fusion_ascend950_amd as mf
+
+    a, b, c = COEFFS
+    gate = accuracy(mf.polar_step(x, a, b, c), x, [COEFFS])
+    step = lambda: mf.polar_step(x, a, b, c)  # noqa: E731
+    settled = settle(step, args.settle_s)
+    sec = time_calls(step, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    return gate, settled, sec
 
 
 def main() -> int:
@@ -252,15 +391,20 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--settle-s", type=float, default=1.0,
+                    help="seconds of headline calls before the warm-up (GPU clock settling)")
+    ap.add_argument("--stage-launches", type=int, default=50,
+                    help="back-to-back launches per stage in the graph-replayed stage timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile", action="store_true",
-                    help="only the headline step loop and three 1 GiB device copies (the "
-                         "calibration kernel of known size), for rocprofv3 runs")
+                    help="only the headline phase (gate, settle, W + K steps), the stage "
+                         "timing of [4096,14336] and [8,512,2048], and three 1 GiB device copies "
+                         "(the calibration kernel of known size), for rocprofv3 runs")
     ap.add_argument("--profile-secondary", action="store_true",
                     help="only the [8,512,2048] step loop, for rocprofv3 runs")
     ap.add_argument("--profile-configs", action="store_true",
-                    help="only a few calls of every BASELINE configuration in turn, for rocprofv3 "
-                         "counter runs")
+                    help="only a few calls of every BASELINE configuration in turn, then three "
+                         "1 GiB device copies (the calibration kernel), for rocprofv3 counter runs")
     ap.add_argument("--profile-muon", action="store_true",
                     help="only a loop of Muon updates of one fp32 [4096,14336] parameter, "
                          "for rocprofv3 runs")
@@ -277,10 +421,8 @@ def main() -> int:
 
     torch.cuda.set_device(0)
     a, b, c = COEFFS
-    out = {}
-
-    # ---- headline: [4096,14336], one step
     batch, m, n = HEADLINE
+
     if args.profile_muon:
         p, g, buf = muon_tensors(m, n)
         sec = time_calls(lambda: mf.muon_update(p, g, buf, lr=MUON_LR, momentum=MUON_MOMENTUM,
@@ -295,6 +437,11 @@ def main() -> int:
             print(json.dumps({"profile": name, "shape": list(shape), "steps_per_call": steps,
                               "us_per_call": round(sec * 1e6, 2)}), flush=True)
             del x
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)  # reads and writes exactly 1 GiB: the counters' calibration
+        torch.cuda.synchronize()
         return 0
     if args.profile_secondary:
         x2 = make_input(SECONDARY, seed=0).cuda()
@@ -302,42 +449,53 @@ def main() -> int:
         print(json.dumps({"profile": "polar_step [8,512,2048]", "steps": args.steps,
                           "us_per_step": round(sec * 1e6, 2)}), flush=True)
         return 0
+
+    # ---- headline: [4096,14336], one step (the driver contract)
     x = make_input((m, n), seed=0).cuda()
+    gate, settled, sec = headline_phase(args, x)
+    flops = credited_flops(batch, m, n)
+    tflops = flops / sec / 1e12
+    print(json.dumps({"phase": "headline", "us_per_step": round(sec * 1e6, 2),
+                      "settle_calls": settled, **gate}), file=sys.stderr, flush=True)
+    st = stage_times(batch, m, n, launches=args.stage_launches)
+    apply_flops = 2 * batch * m * m * n
+    achieved = apply_flops / (st["apply"] * 1e-6) / 1e12
+    b2, m2, n2 = SECONDARY
+    st2 = stage_times(b2, m2, n2, launches=max(args.stage_launches, 100))
     if args.profile:
-        sec = time_calls(lambda: mf.polar_step(x, a, b, c), args.steps, args.warmup)
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)  # reads and writes exactly 1 GiB
         torch.cuda.synchronize()
-        print(json.dumps({"profile": "polar_step [4096,14336]", "steps": args.steps,
-                          "us_per_step": round(sec * 1e6, 2), "copy_bytes": 1 << 30}), flush=True)
+        print(json.dumps({"profile": "polar_step [4096,14336] + stage loops", "steps": args.steps,
+                          "warmup": args.warmup, "settle_calls": settled,
+                          "us_per_step": round(sec * 1e6, 2),
+                          "kernel_us": {k: round(v, 2) for k, v in st.items()},
+                          "secondary_kernel_us": {k: round(v, 2) for k, v in st2.items()},
+                          "stage_launches": [args.stage_launches, max(args.stage_launches, 100)],
+                          "copy_bytes": 1 << 30}), flush=True)
         return 0
-    sec = time_calls(lambda: mf.polar_step(x, a, b, c), args.steps, args.warmup)
-    flops = credited_flops(batch, m, n)
-    tflops = flops / sec / 1e12
-    st = stage_times(batch, m, n, launches=max(10, args.steps // 2))
-    apply_flops = 2 * batch * m * m * n
-    achieved = apply_flops / (st["apply"] * 1e-6) / 1e12
     traffic = read_traffic()
 
-    # ---- secondary: [8,512,2048], one step
-    b2, m2, n2 = SECONDARY
+    # ---- secondary: [8,512,2048], one step (reference method)
     x2 = make_input(SECONDARY, seed=0).cuda()
-    sec2 = time_calls(lambda: mf.polar_step(x2, a, b, c), max(args.steps, 100), args.warmup)
+    gate2 = accuracy(mf.polar_step(x2, a, b, c), x2, [COEFFS])
+    sec2 = reference_method(lambda: mf.polar_step(x2, a, b, c))
     fl2 = credited_flops(b2, m2, n2)
-    st2 = stage_times(b2, m2, n2, launches=max(20, args.steps))
     # bytes that must move at least: X in, Y out; with A and P stored: + 4·B·M²·2 + X re-read
     hbm2 = 2 * b2 * m2 * n2 * 2 + 4 * b2 * m2 * m2 * 2 + b2 * m2 * n2 * 2
 
     # five steps after the normalisation (the reference's examples/five_steps.py loop):
     # one polar_express call vs normalisation in torch + five polar_step calls
     raw = make_input((m, n), seed=1) * 3.0
+
     def reference_loop():
         y = raw / (raw.norm(dim=(-2, -1), keepdim=True) * 1.01 + 1e-6)
         for a_, b_, c_ in mf.COEFFICIENTS:
             y = mf.polar_step(y, a_, b_, c_)
         return y
+
     raw = raw.cuda()
     sec_express = time_calls(lambda: mf.polar_express(raw), 10, 3)
     sec_loop = time_calls(reference_loop, 10, 3)
@@ -351,8 +509,8 @@ def main() -> int:
     del p, g, buf
 
     # PyTorch eager on the same GPU (the reference's comparison point, README.md:172-208)
-    eager = time_calls(lambda: torch_eager(x), 10, 3)
-    eager2 = time_calls(lambda: torch_eager(x2), 50, 5)
+    eager = time_calls(lambda: torch_formula(x, [COEFFS]), 10, 3)
+    eager2 = time_calls(lambda: torch_formula(x2, [COEFFS]), 50, 5)
 
     result = {
         "metric": METRIC,
@@ -376,12 +534,15 @@ def main() -> int:
         },
         "us_per_step": round(sec * 1e6, 2),
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "accuracy": gate,
+        "settle": {"seconds": args.settle_s, "calls": settled},
         "kernel_us": {k: round(v, 2) for k, v in st.items()},
+        "kernel_us_sum": round(sum(st.values()), 2),
         "torch_eager_us": round(eager * 1e6, 2),
         "speedup_vs_torch_eager": round(eager / sec, 3),
         "roofline": {
             "bound": "mfma",
-            "kernel": "stage 3 apply (Y = a·X + P·X)",
+            "kernel": "stage 3 apply (Y = a·X + P·X), 481.0 GFLOP per launch",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
@@ -408,10 +569,13 @@ def main() -> int:
             "tflops": round(fl2 / sec2 / 1e12, 2),
             "pct_bf16_peak": round(100 * fl2 / sec2 / 1e12 / PEAK_BF16_TFLOPS, 2),
             "pct_hbm_peak": round(100 * hbm2 / sec2 / 1e9 / PEAK_HBM_GBS, 2),
+            "accuracy": gate2,
             "kernel_us": {k: round(v, 2) for k, v in st2.items()},
+            "kernel_us_sum": round(sum(st2.values()), 2),
             "torch_eager_us": round(eager2 * 1e6, 2),
             "speedup_vs_torch_eager": round(eager2 / sec2, 3),
         },
+        "run": run_metadata(),
     }
     result["all_configs"] = all_configs()
     if not args.no_cpu_baseline:

@@ -83,3 +83,29 @@ def test_more_than_one_gpu_is_refused(args, env):
                        env={**os.environ, **env}, capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "single-GPU" in r.stderr
+
+
+def test_bench_formula_is_the_reference_formula():
+    """bench.py's own restatement of tests/test_polar_step.py:22-28 (used for its accuracy
+    gates and the PyTorch-eager comparison point) equals the oracle's, step by step."""
+    from oracle import polar_oracle as O
+
+    x = bench.make_input((2, 24, 40), seed=3).float()
+    coeffs = O.COEFFICIENTS[:3]
+    assert torch.allclose(bench.torch_formula(x, coeffs), O.reference_formula_torch(x, coeffs),
+                          rtol=0, atol=1e-6)
+
+
+def test_accuracy_gate_reports_relf():
+    x = bench.make_input((1, 32, 64), seed=4)
+    y = bench.torch_formula(x.float(), [bench.COEFFS]).bfloat16()
+    good = bench.accuracy(y, x, [bench.COEFFS])
+    assert good["gate_6e-2"] == "pass" and good["relF_vs_fp32_formula"] < 1e-2
+    # the all-zero output passes the 6e-2 gate at these magnitudes; relF exposes it
+    zero = bench.accuracy(torch.zeros_like(y), x, [bench.COEFFS])
+    assert zero["relF_vs_fp32_formula"] == pytest.approx(1.0)
+
+
+def test_cpu_info_fields():
+    info = bench.cpu_info()
+    assert set(info) == {"cpu_model", "isa_flags"} and isinstance(info["isa_flags"], list)
