@@ -101,8 +101,14 @@ __device__ __forceinline__ int epi_offset(int row, int col) {
     return row * BN + (epi_pos<BN>(row, col >> 3) << 3) + (col & 7);
 }
 
+// One segment of a workgroup's work: K-steps [kbeg, kend) of output tile
+// tile_base + lt (its stream-K fixup when the tile is cut, and its epilogue when
+// this workgroup completes it).  `smem`, `sink` and `s_arrived` are the caller's
+// LDS: the ring of D K-step slots, the per-wave DMA sink and one arrival word.
 template <int BM, int BN, Stage S, int NW, int D>
-__global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
+__device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem, uint16_t *sink,
+                                               uint32_t *s_arrived_p, int unit, int tile_base,
+                                               int lt, int kbeg, int kend) {
     using Geo = StreamGeom<BM, BN, NW, D>;
     constexpr int kThreads = Geo::kThreads;
     constexpr int WM = BM / 2, WN = BN / (NW / 2);
@@ -129,17 +135,624 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     constexpr bool kEpiLoad = Tr::kEpiOperand && !kAxInLoop;
     // Fragment schedule: a whole K-step ahead for one MFMA per slice, else one slice.
     constexpr bool kStepFrags = kMfmaPerSlice == 1;
+    uint32_t &s_arrived = *s_arrived_p;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int wr = wave & 1, wc = wave >> 1;
+    const int nk = g.k_steps;
+    const uint32_t smem_base = lds_addr(smem);
+    const int64_t tstart = int64_t(lt) * nk;
+    // The thread index is opaque to the optimizer from here on, so the many
+    // per-lane offsets derived from it are formed inside each segment instead
+    // of being kept (and spilled) across the segment loop.
+    int tid = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
+
+    const int tlin = tile_base + lt;
+    const int bt = tlin / g.tiles_per_batch;
+    const int t = tlin - bt * g.tiles_per_batch;
+    int tm, tn;
+    tile_coords(g, Tr::kSymmetric, t, tm, tn);
+    const int row0 = tm * BM, col0 = tn * BN;
+
+    const i32x4 rs_row = make_buffer_rsrc(g.rowop + bt * g.sb_row, g.bytes_row);
+    const i32x4 rs_col = make_buffer_rsrc(g.colop + bt * g.sb_col, g.bytes_col);
+
+    // -------------------------------------------------------- DMA geometry
+    // Per-lane byte offsets of this wave's DMA chunks at K-step 0 (kOob if the
+    // chunk's row/column lies outside the matrix).
+    // K-contiguous panel ([rows][64], 8 rows per 1 KiB instruction) or
+    // N-contiguous panel ([64][rows], 512 / rows K-rows per instruction).
+    constexpr int kARowsPerInstr = 512 / BM, kALanesPerRow = BM / 8;
+    constexpr int kBRowsPerInstr = 512 / BN, kBLanesPerRow = BN / 8;
+    auto a_row = [&](int i) { return 8 * (wave * Geo::kLoadsA + i) + (lane >> 3); };
+    auto a_chunk = [&](int i) { return (lane & 7) ^ kc_swz(a_row(i)); };
+    auto a_krow = [&](int i) {  // N-contiguous row operand
+        return (wave * Geo::kLoadsA + i) * kARowsPerInstr + lane / kALanesPerRow;
+    };
+    auto b_krow = [&](int i) {  // N-contiguous column operand
+        return (wave * Geo::kLoadsB + i) * kBRowsPerInstr + lane / kBLanesPerRow;
+    };
+    auto b_row = [&](int i) { return 8 * (wave * Geo::kLoadsB + i) + (lane >> 3); };
+    auto b_chunk = [&](int i) { return (lane & 7) ^ kc_swz(b_row(i)); };
+
+    uint32_t off_a[Geo::kLoadsA], off_b[Geo::kLoadsB];
+#pragma unroll
+    for (int i = 0; i < Geo::kLoadsA; ++i) {
+        if constexpr (Tr::kRowNC) {
+            const int krow = a_krow(i);
+            const int c = (lane % kALanesPerRow) ^ nc_swz<BM>(krow);
+            const int col = row0 + 8 * c;
+            off_a[i] =
+                col < g.row_rows ? static_cast<uint32_t>((krow * g.ld_row + col) * 2) : kOob;
+        } else {
+            const int gr = row0 + a_row(i);
+            off_a[i] = gr < g.row_rows
+                           ? static_cast<uint32_t>((gr * g.ld_row + 8 * a_chunk(i)) * 2)
+                           : kOob;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < Geo::kLoadsB; ++i) {
+        if constexpr (Tr::kColNC) {
+            const int krow = b_krow(i);
+            const int c = (lane % kBLanesPerRow) ^ nc_swz<BN>(krow);
+            const int col = col0 + 8 * c;
+            off_b[i] =
+                col < g.col_rows ? static_cast<uint32_t>((krow * g.ld_col + col) * 2) : kOob;
+        } else {
+            const int gr = col0 + b_row(i);
+            off_b[i] = gr < g.col_rows
+                           ? static_cast<uint32_t>((gr * g.ld_col + 8 * b_chunk(i)) * 2)
+                           : kOob;
+        }
+    }
+
+    auto a_dst = [&](int slot, int i) {
+        return smem_base + slot * Geo::kStageBytes + (wave * Geo::kLoadsA + i) * 1024;
+    };
+    auto b_dst = [&](int slot, int i) {
+        return smem_base + slot * Geo::kStageBytes + Geo::kABytes +
+               (wave * Geo::kLoadsB + i) * 1024;
+    };
+    auto a_step = [&](int k0) -> uint32_t {
+        return static_cast<uint32_t>((Tr::kRowNC ? k0 * g.ld_row : k0) * 2);
+    };
+    auto b_step = [&](int k0) -> uint32_t {
+        return static_cast<uint32_t>((Tr::kColNC ? k0 * g.ld_col : k0) * 2);
+    };
+    // DMA instruction d (0 .. kLoads-1) of K-step `step` into `slot`, or, when
+    // `live` is false, out-of-range zeros into this wave's sink block (the same
+    // instruction, chosen by scalar operands).  No K masks: the host passes
+    // K-contiguous operands whose rows extend to a multiple of 64 elements with
+    // zeros (padded copies of X, padded A and P), and N-contiguous operands end
+    // at their buffer's num_records, past which the hardware returns zeros.
+    // (An idle instruction whose row is outside the matrix wraps to offset 0:
+    // an in-range read, also into the sink.)
+    const uint32_t sink_base = lds_addr(sink) + wave * 1024;
+    auto dma_one = [&](int d, int step, int slot, bool live) {
+        const int k0 = step * kBK;
+        if (d < Geo::kLoadsA) {
+            const uint32_t koff = live ? a_step(k0) : kOob;
+            dma_16B(rs_row, live ? a_dst(slot, d) : sink_base, off_a[d] + koff);
+        } else {
+            const int i = d - Geo::kLoadsA;
+            const uint32_t koff = live ? b_step(k0) : kOob;
+            dma_16B(rs_col, live ? b_dst(slot, i) : sink_base, off_b[i] + koff);
+        }
+    };
+    auto issue_all = [&](int step, int slot) {
+#pragma unroll
+        for (int d = 0; d < Geo::kLoads; ++d) dma_one(d, step, slot, true);
+    };
+
+    // Epilogue operand tile (A for poly, X for apply) -> LDS ring slot `eslot`
+    // (the tile may span several slots from slot 0), rows/cols outside the
+    // matrix read as zero.
+    auto issue_epi = [&](int eslot) {
+        if constexpr (kEpiLoad) {
+            const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
+            constexpr int kChunksPerRow = BN / 8;
+#pragma unroll
+            for (int d = 0; d < Geo::kEpiLoads; ++d) {
+                // LDS chunk q of the tile (row q / kChunksPerRow, position q %
+                // kChunksPerRow) receives global chunk epi_pos(row, position).
+                const int blk = wave * Geo::kEpiLoads + d;
+                const int q = blk * 64 + lane;
+                const int row = q / kChunksPerRow;
+                const int c = epi_pos<BN>(row, q - row * kChunksPerRow);
+                const int gr = row0 + row, gc = col0 + 8 * c;
+                const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
+                                       ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
+                                       : kOob;
+                dma_16B(rs_epi, smem_base + eslot * Geo::kStageBytes + blk * 1024, v);
+            }
+        }
+    };
+
+    // -------------------------------------------------------- main loop
+    f32x16 acc[SM][SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // MFMA operand fragments of one k16 slice, double-buffered in registers.
+    // Fragment f of k16 slice kk from `slot`: f < SM row-operand fragment f,
+    // else column-operand fragment f - SM.
+    auto load_frag = [&](int slot, int kk, int f, bf16x8 (&fr)[SM], bf16x8 (&fc)[SN]) {
+        const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
+        const uint16_t *bs = as + Geo::kABytes / 2;
+        if (f < SM) {
+            if constexpr (Tr::kRowNC)
+                fr[f] = frag_nc_tr<BM>(as, wr * WM + f * 32 + ((lane >> 4) & 1) * 16, kk, lane);
+            else
+                fr[f] = frag_kc(as, wr * WM + f * 32 + (lane & 31), kk, lane);
+        } else {
+            const int j = f - SM;
+            if constexpr (Tr::kColNC)
+                fc[j] = frag_nc_tr<BN>(bs, wc * WN + j * 32 + ((lane >> 4) & 1) * 16, kk, lane);
+            else
+                fc[j] = frag_kc(bs, wc * WN + j * 32 + (lane & 31), kk, lane);
+        }
+    };
+    auto load_frags = [&](int slot, int kk, bf16x8 (&fr)[SM], bf16x8 (&fc)[SN]) {
+#pragma unroll
+        for (int f = 0; f < SM + SN; ++f) load_frag(slot, kk, f, fr, fc);
+    };
+    // a·X into the accumulators from the panel of global K-step kg in `slot`,
+    // when that step's 64 K-values are 64 of this tile's rows (apply: X rows;
+    // the column panel [64][BN] holds X[k][col0 + c]) or columns (apply-right:
+    // X columns; the row panel [BM][64] holds X[row0 + r][k]).  Each lane adds
+    // the 4 consecutive values its accumulator elements 4q..4q+3 cover, once
+    // per output element over the whole K loop.
+    auto add_ax = [&](int slot, int kg) {
+        if constexpr (kAxInLoop) {
+            const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
+            const uint16_t *bs = as + Geo::kABytes / 2;
+            const float a = g.s_epi;
+            auto fma4 = [&](f32x16 &acc_ij, int q, u32x2 v) {
+                float x[4];
+                unpack4(v, x);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc_ij[4 * q + t] = fmaf(a, x[t], acc_ij[4 * q + t]);
+            };
+            if constexpr (S == Stage::Apply) {
+                const int rel = kg * kBK - row0;  // tile row of the step's first K-row
+                if (rel < 0 || rel >= BM) return;
+#pragma unroll
+                for (int i = 0; i < SM; ++i) {
+                    const int rb = wr * WM + 32 * i;
+                    if (rb < rel || rb >= rel + kBK) continue;
+                    const int kr = rb - rel + (lane & 31);
+#pragma unroll
+                    for (int j = 0; j < SN; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int c = wc * WN + 32 * j + 8 * q + 4 * (lane >> 5);
+                            fma4(acc[i][j], q,
+                                 *reinterpret_cast<const u32x2 *>(
+                                     bs + nc_offset<BN>(kr, c >> 3) + (c & 7)));
+                        }
+                }
+            } else {
+                const int rel = kg * kBK - col0;  // tile column of the step's first K
+                if (rel < 0 || rel >= BN) return;
+#pragma unroll
+                for (int j = 0; j < SN; ++j) {
+                    const int cb = wc * WN + 32 * j;
+                    if (cb < rel || cb >= rel + kBK) continue;
+#pragma unroll
+                    for (int i = 0; i < SM; ++i) {
+                        const int r = wr * WM + 32 * i + (lane & 31);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int kc = cb - rel + 8 * q + 4 * (lane >> 5);
+                            fma4(acc[i][j], q,
+                                 *reinterpret_cast<const u32x2 *>(
+                                     as + kc_offset(r, kc >> 3) + (kc & 7)));
+                        }
+                    }
+                }
+            }
+        }
+    };
+    auto mfmas = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN]) {
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j) acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
+    };
+    // Last slice of a step: its MFMAs with the DMA of panel `step` interleaved,
+    // about kLoads / kMfmaPerSlice instructions after each MFMA (into the sink
+    // when `live` is false: the panel would be past the segment's end; a
+    // branch around each DMA instead cost 3-4% of the step at 4096 x 14336),
+    // and the next step's slice-0 fragment reads (from slot `nslot`, complete
+    // once the step's barrier has passed) issued one after each MFMA too (0.7%
+    // faster at 4096 x 14336 than reading them all first).
+    auto mfmas_with_dma_frags = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN], int step,
+                                    int slot_, bool live, int nslot,
+                                    bf16x8 (&nfr)[SM], bf16x8 (&nfc)[SN]) {
+#pragma unroll
+        for (int m = 0; m < kMfmaPerSlice; ++m) {
+            const int i = m / SN, j = m % SN;
+            acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (m < SM + SN) load_frag(nslot, 0, m, nfr, nfc);
+#pragma unroll
+            for (int d = m * Geo::kLoads / kMfmaPerSlice;
+                 d < (m + 1) * Geo::kLoads / kMfmaPerSlice; ++d)
+                dma_one(d, step, slot_, live);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int f = kMfmaPerSlice; f < SM + SN; ++f) load_frag(nslot, 0, f, nfr, nfc);
+    };
+    static_assert(kBK / 16 == 4, "schedule below is written for four k16 slices per step");
+
+    // Schedule per K-step k (slot k % kStages), slices s0..s3 of 16 K-values:
+    //   frags(s1) | mfma(s0) | frags(s2) | mfma(s1) | frags(s3) | mfma(s2) |
+    //   wait panel k+1, barrier | frags(next s0) | mfma(s3) + DMA panel k+kStages -> slot
+    // Within each "frags | mfma" pair the fragment reads are issued one after
+    // each MFMA (1-2% faster than all reads first at 4096 x 14336).
+    // The barrier sits where every wave has read all of step k's slot into
+    // registers; panels k+2 .. k+kStages-1 may still be in flight there.
+    // With the epilogue tile in a slot (kEpiInSlot), the first step that issues
+    // no panel (k = nkl - kStages) issues the epilogue operand tile into its
+    // slot instead; every later wait lets those loads stay in flight.
+    const int nkl = kend - kbeg;
+    constexpr bool kEpiPrefetch = kEpiLoad && Geo::kEpiInSlot;
+    const int npro = nkl < kStages ? nkl : kStages;
+    for (int i = 0; i < npro; ++i) issue_all(kbeg + i, i);
+    int epi_slot = 0;
+    if constexpr (kEpiPrefetch) {
+        if (nkl < kStages) {
+            epi_slot = nkl;  // a slot the K loop never fills
+            issue_epi(epi_slot);
+            wait_panels_barrier<Geo::kLoads, kStages, Geo::kEpiLoads>(npro - 1);
+        } else {
+            epi_slot = (nkl - kStages) % kStages;
+            wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
+        }
+    } else {
+        wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
+    }
+    int slot = 0;
+    if constexpr (kStepFrags) {
+        // One MFMA per k16 slice (32x32 wave tiles): a slice's fragment reads
+        // cannot hide behind the single MFMA issued before them, so every slice
+        // would wait out the LDS latency.  Instead all fragments of step k+1 are
+        // read right after step k's barrier, while step k's MFMAs (on fragments
+        // read one step earlier) run.  MFMAs and a·X additions keep the order of
+        // the schedule below, so results are the same bits.
+        bf16x8 ar[4][SM], ac[4][SN], br[4][SM], bc[4][SN];
+        auto read_step = [&](int sl, bf16x8 (&r)[4][SM], bf16x8 (&c)[4][SN]) {
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) load_frags(sl, kk, r[kk], c[kk]);
+        };
+        auto step = [&](int k, const bf16x8 (&r)[4][SM], const bf16x8 (&c)[4][SN],
+                        bf16x8 (&nr)[4][SM], bf16x8 (&nc)[4][SN]) {
+            const int next = slot + 1 == kStages ? 0 : slot + 1;
+            // the same waits as the schedule below: panel k+1, before this
+            // step's DMA group
+            const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+            if (kEpiPrefetch && k > nkl - kStages)
+                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
+            else
+                wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
+            read_step(next, nr, nc);  // stale on the last step, not used
+            __builtin_amdgcn_sched_barrier(0);
+            constexpr int kM = 4 * kMfmaPerSlice;
+            const int dstep = kbeg + k + kStages;
+            const bool live = k + kStages < nkl;
+#pragma unroll
+            for (int m = 0; m < kM; ++m) {
+                const int kk = m / kMfmaPerSlice, ij = m % kMfmaPerSlice;
+                acc[ij / SN][ij % SN] =
+                    mfma_32x32x16(c[kk][ij % SN], r[kk][ij / SN], acc[ij / SN][ij % SN]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int d = m * Geo::kLoads / kM; d < (m + 1) * Geo::kLoads / kM; ++d)
+                    dma_one(d, dstep, slot, live);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (kAxInLoop) {
+                if (k + 1 < nkl) add_ax(next, kbeg + k + 1);
+            }
+            if constexpr (kEpiPrefetch) {
+                if (k == nkl - kStages) issue_epi(epi_slot);
+            }
+            slot = next;
+        };
+        if constexpr (kAxInLoop) add_ax(0, kbeg);
+        read_step(0, ar, ac);
+        int k = 0;
+        for (; k + 1 < nkl; k += 2) {
+            step(k, ar, ac, br, bc);
+            step(k + 1, br, bc, ar, ac);
+        }
+        if (k < nkl) step(k, ar, ac, br, bc);
+    } else {
+        bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
+        load_frags(0, 0, fr0, fc0);
+        for (int k = 0; k < nkl; ++k) {
+            const int next = slot + 1 == kStages ? 0 : slot + 1;
+            if constexpr (kAxInLoop) add_ax(slot, kbeg + k);
+            load_frags(slot, 1, fr1, fc1);
+            mfmas(fr0, fc0);
+            for (int z = 0; z < kMfmaPerSlice; ++z) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_frags(slot, 2, fr0, fc0);
+            mfmas(fr1, fc1);
+            for (int z = 0; z < kMfmaPerSlice; ++z) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_frags(slot, 3, fr1, fc1);
+            mfmas(fr0, fc0);
+            for (int z = 0; z < kMfmaPerSlice; ++z) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // Wait for panel k+1.  The DMA groups issued after it (each step issues
+            // one, to the ring or the sink; the prologue issued npro) may stay in
+            // flight: prologue panels k+2 .. npro-1 and the groups of steps
+            // k+2-kStages .. k-1, at most kStages-2 groups (plus the epilogue tile
+            // once issued).  Unconditional, also on the last step (nothing needed is
+            // in flight then, and the fragments read from the stale slot are not
+            // used): a branch around these LDS reads makes the compiler's wait
+            // counts on the join below assume none were issued, and the slice-3
+            // MFMAs would then wait for all of them.
+            const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+            if (kEpiPrefetch && k > nkl - kStages)
+                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
+            else
+                wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
+            mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
+                                 fc0);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kEpiPrefetch) {
+                if (k == nkl - kStages) issue_epi(epi_slot);
+            }
+            slot = next;
+        }
+    }
+    // All waves are done with the ring (and no DMA is outstanding).
+    wait_vm_barrier<0>();
+
+    // -------------------------------------------------------- stream-K fixup
+    bool epi_issued = false;
+    if (kbeg != 0 || kend != nk) {
+        // This tile is cut between units u0 .. u1.  Each contributor but the
+        // last stores its fp32 partial and counts itself in; the last one to
+        // arrive forms p(u1) + p(u1 - 1) + ... + p(u0) in that fixed order (so
+        // results do not depend on arrival order) and runs the epilogue.
+        const int u0 = sk_unit_of(g, tstart), u1 = sk_unit_of(g, tstart + nk - 1);
+        const uint32_t others = static_cast<uint32_t>(u1 - u0);
+        uint64_t *cnt = g.counters + lt;
+        const uint64_t tok = uint64_t(g.token) << 32;
+        auto count_of = [&](uint64_t w) -> uint32_t {
+            return (w & 0xffffffff00000000ull) == tok ? static_cast<uint32_t>(w) : 0u;
+        };
+        // Partials and counters are accessed device-coherently (sc1 stores and
+        // loads, agent-scope atomics), so no whole-cache write-back or
+        // invalidate is needed: a contributor's stores are complete before its
+        // count is added, and the last contributor reads them after seeing
+        // every count.  The L2 contents the other workgroups are streaming
+        // from stay intact.
+        constexpr int kSc1 = 16;  // cache-policy bits of a device-scope access
+        const int64_t slot_bytes = int64_t(BM) * BN * 4;
+        const __amdgpu_buffer_rsrc_t rs_part =
+            __builtin_amdgcn_make_buffer_rsrc(g.partials, 0, 0x7fffffff, 0x00020000);
+        auto lane_base = [&](int u) {
+            return static_cast<uint32_t>(int64_t(sk_slot(u, lt)) * slot_bytes) + tid * 16;
+        };
+        // Slot layout: 16-byte chunk c = (i * SN + j) * 4 + q of every thread,
+        // thread-minor, so each access instruction covers 1 KiB contiguously.
+        constexpr uint32_t kChunkStride = kThreads * 16;
+        auto store_own = [&]() {
+            const uint32_t base = lane_base(unit);
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+#pragma unroll
+                for (int j = 0; j < SN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                  acc[i][j][4 * q + 3]},
+                            rs_part, base + ((i * SN + j) * 4 + q) * kChunkStride, 0, kSc1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        };
+        if (tid == 0)
+            s_arrived = count_of(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        __syncthreads();
+        bool last = __builtin_amdgcn_readfirstlane(s_arrived) == others;
+        bool stored = false;
+        if (!last) {
+            store_own();
+            stored = true;
+            __syncthreads();
+            if (tid == 0) {
+                // count this unit in: compare-and-swap, starting from zero when the
+                // word holds another launch's token (each failed exchange means
+                // another contributor got in, so at most two retries)
+                uint64_t old = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                uint32_t before = count_of(old);
+                while (!__hip_atomic_compare_exchange_strong(
+                    cnt, &old, tok | (before + 1u), __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                    __HIP_MEMORY_SCOPE_AGENT))
+                    before = count_of(old);
+                s_arrived = before;
+            }
+            __syncthreads();
+            last = __builtin_amdgcn_readfirstlane(s_arrived) == others;
+        }
+        if (!last) return;
+        // Every other contributor has counted itself in: the word is this
+        // unit's alone now.  Leave a zero count under this launch's token (a
+        // replay of the launch reuses the token).
+        if (tid == 0) __hip_atomic_store(cnt, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // The epilogue operand tile (poly's A tile, which fills the idle ring) is
+        // fetched now, so that its round trip overlaps the partials' reads
+        // instead of following them.
+        if constexpr (kEpiLoad && !kEpiPrefetch) {
+            issue_epi(0);
+            epi_issued = true;
+        }
+        // Own partial first or second in the order: add the others to it in
+        // place (x + y == y + x).  Further back: start from p(u1) in memory.
+        const bool from_memory = u1 - unit >= 2;
+        if (from_memory && !stored) store_own();  // read back by the same lanes
+        // Partials are read a row-block (16 chunks per lane) at a time, the
+        // next block's loads in flight while the current one is added.
+        auto add_partial = [&](int u, bool assign) {
+            const uint32_t base = lane_base(u);
+            // blocks of kBlk accumulator tiles (i, j), the next block's loads in
+            // flight while one is added (one row-block of SN tiles; one tile
+            // for the 256-register accumulators)
+            constexpr int kBlk = kBigAcc ? 1 : SN;
+            constexpr int kBlocks = SM * SN / kBlk;
+            f32x4 x[2][kBlk * 4];
+            auto load_block = [&](int blk, f32x4 (&dst)[kBlk * 4]) {
+#pragma unroll
+                for (int c = 0; c < kBlk * 4; ++c)
+                    dst[c] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rs_part, base + (blk * kBlk * 4 + c) * kChunkStride, 0, kSc1);
+            };
+            load_block(0, x[0]);
+#pragma unroll
+            for (int blk = 0; blk < kBlocks; ++blk) {
+                if (blk + 1 < kBlocks) load_block(blk + 1, x[(blk + 1) & 1]);
+#pragma unroll
+                for (int t = 0; t < kBlk; ++t) {
+                    const int ij = blk * kBlk + t, i = ij / SN, j = ij % SN;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[i][j][4 * q + e] = assign ? x[blk & 1][t * 4 + q][e]
+                                                          : acc[i][j][4 * q + e] +
+                                                                x[blk & 1][t * 4 + q][e];
+                }
+            }
+        };
+        if (from_memory) add_partial(u1, true);
+        for (int u = from_memory ? u1 - 1 : u1; u >= u0; --u)
+            if (from_memory || u != unit) add_partial(u, false);
+    }
+
+    // -------------------------------------------------------- epilogue
+    uint16_t *tile = smem + epi_slot * (Geo::kStageBytes / 2);
+    uint16_t *out = g.out + bt * g.sb_out;
+    const bool diag = Tr::kSymmetric && (tm == tn);
+
+    if constexpr (kEpiLoad && !kEpiPrefetch) {
+        if (!epi_issued) issue_epi(0);
+        wait_vm_barrier<0>();
+    }
+
+    // Each lane turns its accumulators into bf16 results in place.
+#pragma unroll
+    for (int i = 0; i < SM; ++i) {
+        const int r = wr * WM + i * 32 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
+                u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
+                float e[4] = {0.f, 0.f, 0.f, 0.f};
+                uint16_t h[4];
+                if constexpr (kAxInLoop) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) h[t] = f32_to_bf16_bits(acc[i][j][4 * q + t]);
+                } else {
+                    if constexpr (kEpiLoad) unpack4(*p, e);
+                    epilogue_values<S>(acc[i][j], q, e, g, h);
+                }
+                *p = pack4(h);
+            }
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // Coalesced store of the tile: 16-byte chunks, consecutive threads along a row.
+    constexpr int kChunksPerRow = BN / 8;
+    for (int idx = tid; idx < BM * kChunksPerRow; idx += kThreads) {
+        const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
+        const int gr = row0 + row, gc = col0 + 8 * c;
+        if constexpr (!Tr::kSymmetric) {
+            if (gr >= g.out_rows || gc >= g.out_cols) continue;
+        }
+        u32x4 v;
+        if (!diag) {
+            v = *reinterpret_cast<const u32x4 *>(tile + epi_offset<BN>(row, 8 * c));
+        } else {
+            // Diagonal tile: element (r, c) comes from the upper-triangle source
+            // min/max(r, c), so the stored matrix is bitwise symmetric.
+            uint32_t hh[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int col = 8 * c + e;
+                hh[e] = row <= col ? tile[epi_offset<BN>(row, col)]
+                                   : tile[epi_offset<BN>(col, row)];
+            }
+            v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
+                      hh[6] | (hh[7] << 16)};
+        }
+        if (Tr::kSymmetric) {
+            *reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc) = v;
+        } else if (g.out_vec) {
+            // Y is not read again by this step: a non-temporal store keeps it from
+            // displacing operand panels in L2 ([8,512,2048] 46.8 -> 44.4 us; the
+            // large shapes unchanged; A and P, read by the next stage, stay cached)
+            __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc));
+        } else {
+            // rows of n % 8 != 0 elements: 2-byte stores up to the last column
+            uint16_t *dst = out + gr * g.ld_out + gc;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (gc + e < g.out_cols) dst[e] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
+        }
+    }
+
+    // Mirrored store (symmetric stages, off-diagonal tiles): row c of the
+    // mirror tile is column c of this tile; consecutive threads walk along it.
+    if constexpr (Tr::kSymmetric) {
+        if (!diag) {
+            constexpr int kMirrorChunks = BM / 8;  // 16-byte chunks per mirror row
+            for (int idx = tid; idx < BN * kMirrorChunks; idx += kThreads) {
+                const int mc = idx / kMirrorChunks, rb = idx % kMirrorChunks;
+                uint32_t hh[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hh[e] = tile[epi_offset<BN>(8 * rb + e, mc)];
+                const u32x4 v{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16),
+                              hh[4] | (hh[5] << 16), hh[6] | (hh[7] << 16)};
+                *reinterpret_cast<u32x4 *>(out + (col0 + mc) * g.ld_out + row0 + 8 * rb) = v;
+            }
+        }
+    }
+}
+
+template <int BM, int BN, Stage S, int NW, int D>
+__global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
+    using Geo = StreamGeom<BM, BN, NW, D>;
+    constexpr int kStages = Geo::kStages;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * Geo::kStageBytes / 2];
     // 1 KiB per wave that the ring's idle DMA instructions write (out-of-range
     // offsets: zeros, no memory traffic) in the last kStages steps of a segment,
     // so that every step issues the same instructions: no branch around them.
     __shared__ __attribute__((aligned(1024))) uint16_t sink[NW * 512];
     __shared__ uint32_t s_arrived;
-
-    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-    const int wr = wave & 1, wc = wave >> 1;
     const int nk = g.k_steps;
-    const uint32_t smem_base = lds_addr(smem);
 
     // Work of this workgroup: iterations [it_lo, it_hi) of tiles tile_base + i / nk
     // (polar_schedule.hpp: XCD-contiguous whole tiles, then the stream-K units).
@@ -159,605 +772,8 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         const int kbeg = static_cast<int>(lo - tstart), kend = static_cast<int>(hi - tstart);
         if (hi != it_hi) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         hi = lo;
-        // The thread index is opaque to the optimizer from here on, so the many
-        // per-lane offsets derived from it are formed inside each segment instead
-        // of being kept (and spilled) across the segment loop.
-        int tid = static_cast<int>(threadIdx.x);
-        asm volatile("" : "+v"(tid));
-        const int lane = tid & 63;
-
-        const int tlin = tile_base + lt;
-        const int bt = tlin / g.tiles_per_batch;
-        const int t = tlin - bt * g.tiles_per_batch;
-        int tm, tn;
-        tile_coords(g, Tr::kSymmetric, t, tm, tn);
-        const int row0 = tm * BM, col0 = tn * BN;
-
-        const i32x4 rs_row = make_buffer_rsrc(g.rowop + bt * g.sb_row, g.bytes_row);
-        const i32x4 rs_col = make_buffer_rsrc(g.colop + bt * g.sb_col, g.bytes_col);
-
-        // -------------------------------------------------------- DMA geometry
-        // Per-lane byte offsets of this wave's DMA chunks at K-step 0 (kOob if the
-        // chunk's row/column lies outside the matrix).
-        // K-contiguous panel ([rows][64], 8 rows per 1 KiB instruction) or
-        // N-contiguous panel ([64][rows], 512 / rows K-rows per instruction).
-        constexpr int kARowsPerInstr = 512 / BM, kALanesPerRow = BM / 8;
-        constexpr int kBRowsPerInstr = 512 / BN, kBLanesPerRow = BN / 8;
-        auto a_row = [&](int i) { return 8 * (wave * Geo::kLoadsA + i) + (lane >> 3); };
-        auto a_chunk = [&](int i) { return (lane & 7) ^ kc_swz(a_row(i)); };
-        auto a_krow = [&](int i) {  // N-contiguous row operand
-            return (wave * Geo::kLoadsA + i) * kARowsPerInstr + lane / kALanesPerRow;
-        };
-        auto b_krow = [&](int i) {  // N-contiguous column operand
-            return (wave * Geo::kLoadsB + i) * kBRowsPerInstr + lane / kBLanesPerRow;
-        };
-        auto b_row = [&](int i) { return 8 * (wave * Geo::kLoadsB + i) + (lane >> 3); };
-        auto b_chunk = [&](int i) { return (lane & 7) ^ kc_swz(b_row(i)); };
-
-        uint32_t off_a[Geo::kLoadsA], off_b[Geo::kLoadsB];
-#pragma unroll
-        for (int i = 0; i < Geo::kLoadsA; ++i) {
-            if constexpr (Tr::kRowNC) {
-                const int krow = a_krow(i);
-                const int c = (lane % kALanesPerRow) ^ nc_swz<BM>(krow);
-                const int col = row0 + 8 * c;
-                off_a[i] =
-                    col < g.row_rows ? static_cast<uint32_t>((krow * g.ld_row + col) * 2) : kOob;
-            } else {
-                const int gr = row0 + a_row(i);
-                off_a[i] = gr < g.row_rows
-                               ? static_cast<uint32_t>((gr * g.ld_row + 8 * a_chunk(i)) * 2)
-                               : kOob;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < Geo::kLoadsB; ++i) {
-            if constexpr (Tr::kColNC) {
-                const int krow = b_krow(i);
-                const int c = (lane % kBLanesPerRow) ^ nc_swz<BN>(krow);
-                const int col = col0 + 8 * c;
-                off_b[i] =
-                    col < g.col_rows ? static_cast<uint32_t>((krow * g.ld_col + col) * 2) : kOob;
-            } else {
-                const int gr = col0 + b_row(i);
-                off_b[i] = gr < g.col_rows
-                               ? static_cast<uint32_t>((gr * g.ld_col + 8 * b_chunk(i)) * 2)
-                               : kOob;
-            }
-        }
-
-        auto a_dst = [&](int slot, int i) {
-            return smem_base + slot * Geo::kStageBytes + (wave * Geo::kLoadsA + i) * 1024;
-        };
-        auto b_dst = [&](int slot, int i) {
-            return smem_base + slot * Geo::kStageBytes + Geo::kABytes +
-                   (wave * Geo::kLoadsB + i) * 1024;
-        };
-        auto a_step = [&](int k0) -> uint32_t {
-            return static_cast<uint32_t>((Tr::kRowNC ? k0 * g.ld_row : k0) * 2);
-        };
-        auto b_step = [&](int k0) -> uint32_t {
-            return static_cast<uint32_t>((Tr::kColNC ? k0 * g.ld_col : k0) * 2);
-        };
-        // DMA instruction d (0 .. kLoads-1) of K-step `step` into `slot`, or, when
-        // `live` is false, out-of-range zeros into this wave's sink block (the same
-        // instruction, chosen by scalar operands).  No K masks: the host passes
-        // K-contiguous operands whose rows extend to a multiple of 64 elements with
-        // zeros (padded copies of X, padded A and P), and N-contiguous operands end
-        // at their buffer's num_records, past which the hardware returns zeros.
-        // (An idle instruction whose row is outside the matrix wraps to offset 0:
-        // an in-range read, also into the sink.)
-        const uint32_t sink_base = lds_addr(sink) + wave * 1024;
-        auto dma_one = [&](int d, int step, int slot, bool live) {
-            const int k0 = step * kBK;
-            if (d < Geo::kLoadsA) {
-                const uint32_t koff = live ? a_step(k0) : kOob;
-                dma_16B(rs_row, live ? a_dst(slot, d) : sink_base, off_a[d] + koff);
-            } else {
-                const int i = d - Geo::kLoadsA;
-                const uint32_t koff = live ? b_step(k0) : kOob;
-                dma_16B(rs_col, live ? b_dst(slot, i) : sink_base, off_b[i] + koff);
-            }
-        };
-        auto issue_all = [&](int step, int slot) {
-#pragma unroll
-            for (int d = 0; d < Geo::kLoads; ++d) dma_one(d, step, slot, true);
-        };
-
-        // Epilogue operand tile (A for poly, X for apply) -> LDS ring slot `eslot`
-        // (the tile may span several slots from slot 0), rows/cols outside the
-        // matrix read as zero.
-        auto issue_epi = [&](int eslot) {
-            if constexpr (kEpiLoad) {
-                const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
-                constexpr int kChunksPerRow = BN / 8;
-#pragma unroll
-                for (int d = 0; d < Geo::kEpiLoads; ++d) {
-                    // LDS chunk q of the tile (row q / kChunksPerRow, position q %
-                    // kChunksPerRow) receives global chunk epi_pos(row, position).
-                    const int blk = wave * Geo::kEpiLoads + d;
-                    const int q = blk * 64 + lane;
-                    const int row = q / kChunksPerRow;
-                    const int c = epi_pos<BN>(row, q - row * kChunksPerRow);
-                    const int gr = row0 + row, gc = col0 + 8 * c;
-                    const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
-                                           ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
-                                           : kOob;
-                    dma_16B(rs_epi, smem_base + eslot * Geo::kStageBytes + blk * 1024, v);
-                }
-            }
-        };
-
-        // -------------------------------------------------------- main loop
-        f32x16 acc[SM][SN];
-#pragma unroll
-        for (int i = 0; i < SM; ++i)
-#pragma unroll
-            for (int j = 0; j < SN; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-        // MFMA operand fragments of one k16 slice, double-buffered in registers.
-        // Fragment f of k16 slice kk from `slot`: f < SM row-operand fragment f,
-        // else column-operand fragment f - SM.
-        auto load_frag = [&](int slot, int kk, int f, bf16x8 (&fr)[SM], bf16x8 (&fc)[SN]) {
-            const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
-            const uint16_t *bs = as + Geo::kABytes / 2;
-            if (f < SM) {
-                if constexpr (Tr::kRowNC)
-                    fr[f] = frag_nc_tr<BM>(as, wr * WM + f * 32 + ((lane >> 4) & 1) * 16, kk, lane);
-                else
-                    fr[f] = frag_kc(as, wr * WM + f * 32 + (lane & 31), kk, lane);
-            } else {
-                const int j = f - SM;
-                if constexpr (Tr::kColNC)
-                    fc[j] = frag_nc_tr<BN>(bs, wc * WN + j * 32 + ((lane >> 4) & 1) * 16, kk, lane);
-                else
-                    fc[j] = frag_kc(bs, wc * WN + j * 32 + (lane & 31), kk, lane);
-            }
-        };
-        auto load_frags = [&](int slot, int kk, bf16x8 (&fr)[SM], bf16x8 (&fc)[SN]) {
-#pragma unroll
-            for (int f = 0; f < SM + SN; ++f) load_frag(slot, kk, f, fr, fc);
-        };
-        // a·X into the accumulators from the panel of global K-step kg in `slot`,
-        // when that step's 64 K-values are 64 of this tile's rows (apply: X rows;
-        // the column panel [64][BN] holds X[k][col0 + c]) or columns (apply-right:
-        // X columns; the row panel [BM][64] holds X[row0 + r][k]).  Each lane adds
-        // the 4 consecutive values its accumulator elements 4q..4q+3 cover, once
-        // per output element over the whole K loop.
-        auto add_ax = [&](int slot, int kg) {
-            if constexpr (kAxInLoop) {
-                const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
-                const uint16_t *bs = as + Geo::kABytes / 2;
-                const float a = g.s_epi;
-                auto fma4 = [&](f32x16 &acc_ij, int q, u32x2 v) {
-                    float x[4];
-                    unpack4(v, x);
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) acc_ij[4 * q + t] = fmaf(a, x[t], acc_ij[4 * q + t]);
-                };
-                if constexpr (S == Stage::Apply) {
-                    const int rel = kg * kBK - row0;  // tile row of the step's first K-row
-                    if (rel < 0 || rel >= BM) return;
-#pragma unroll
-                    for (int i = 0; i < SM; ++i) {
-                        const int rb = wr * WM + 32 * i;
-                        if (rb < rel || rb >= rel + kBK) continue;
-                        const int kr = rb - rel + (lane & 31);
-#pragma unroll
-                        for (int j = 0; j < SN; ++j)
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                const int c = wc * WN + 32 * j + 8 * q + 4 * (lane >> 5);
-                                fma4(acc[i][j], q,
-                                     *reinterpret_cast<const u32x2 *>(
-                                         bs + nc_offset<BN>(kr, c >> 3) + (c & 7)));
-                            }
-                    }
-                } else {
-                    const int rel = kg * kBK - col0;  // tile column of the step's first K
-                    if (rel < 0 || rel >= BN) return;
-#pragma unroll
-                    for (int j = 0; j < SN; ++j) {
-                        const int cb = wc * WN + 32 * j;
-                        if (cb < rel || cb >= rel + kBK) continue;
-#pragma unroll
-                        for (int i = 0; i < SM; ++i) {
-                            const int r = wr * WM + 32 * i + (lane & 31);
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                const int kc = cb - rel + 8 * q + 4 * (lane >> 5);
-                                fma4(acc[i][j], q,
-                                     *reinterpret_cast<const u32x2 *>(
-                                         as + kc_offset(r, kc >> 3) + (kc & 7)));
-                            }
-                        }
-                    }
-                }
-            }
-        };
-        auto mfmas = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN]) {
-#pragma unroll
-            for (int i = 0; i < SM; ++i)
-#pragma unroll
-                for (int j = 0; j < SN; ++j) acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
-        };
-        // Last slice of a step: its MFMAs with the DMA of panel `step` interleaved,
-        // about kLoads / kMfmaPerSlice instructions after each MFMA (into the sink
-        // when `live` is false: the panel would be past the segment's end; a
-        // branch around each DMA instead cost 3-4% of the step at 4096 x 14336),
-        // and the next step's slice-0 fragment reads (from slot `nslot`, complete
-        // once the step's barrier has passed) issued one after each MFMA too (0.7%
-        // faster at 4096 x 14336 than reading them all first).
-        auto mfmas_with_dma_frags = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN], int step,
-                                        int slot_, bool live, int nslot,
-                                        bf16x8 (&nfr)[SM], bf16x8 (&nfc)[SN]) {
-#pragma unroll
-            for (int m = 0; m < kMfmaPerSlice; ++m) {
-                const int i = m / SN, j = m % SN;
-                acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
-                __builtin_amdgcn_sched_barrier(0);
-                if (m < SM + SN) load_frag(nslot, 0, m, nfr, nfc);
-#pragma unroll
-                for (int d = m * Geo::kLoads / kMfmaPerSlice;
-                     d < (m + 1) * Geo::kLoads / kMfmaPerSlice; ++d)
-                    dma_one(d, step, slot_, live);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-#pragma unroll
-            for (int f = kMfmaPerSlice; f < SM + SN; ++f) load_frag(nslot, 0, f, nfr, nfc);
-        };
-        static_assert(kBK / 16 == 4, "schedule below is written for four k16 slices per step");
-
-        // Schedule per K-step k (slot k % kStages), slices s0..s3 of 16 K-values:
-        //   frags(s1) | mfma(s0) | frags(s2) | mfma(s1) | frags(s3) | mfma(s2) |
-        //   wait panel k+1, barrier | frags(next s0) | mfma(s3) + DMA panel k+kStages -> slot
-        // Within each "frags | mfma" pair the fragment reads are issued one after
-        // each MFMA (1-2% faster than all reads first at 4096 x 14336).
-        // The barrier sits where every wave has read all of step k's slot into
-        // registers; panels k+2 .. k+kStages-1 may still be in flight there.
-        // With the epilogue tile in a slot (kEpiInSlot), the first step that issues
-        // no panel (k = nkl - kStages) issues the epilogue operand tile into its
-        // slot instead; every later wait lets those loads stay in flight.
-        const int nkl = kend - kbeg;
-        constexpr bool kEpiPrefetch = kEpiLoad && Geo::kEpiInSlot;
-        const int npro = nkl < kStages ? nkl : kStages;
-        for (int i = 0; i < npro; ++i) issue_all(kbeg + i, i);
-        int epi_slot = 0;
-        if constexpr (kEpiPrefetch) {
-            if (nkl < kStages) {
-                epi_slot = nkl;  // a slot the K loop never fills
-                issue_epi(epi_slot);
-                wait_panels_barrier<Geo::kLoads, kStages, Geo::kEpiLoads>(npro - 1);
-            } else {
-                epi_slot = (nkl - kStages) % kStages;
-                wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
-            }
-        } else {
-            wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
-        }
-        int slot = 0;
-        if constexpr (kStepFrags) {
-            // One MFMA per k16 slice (32x32 wave tiles): a slice's fragment reads
-            // cannot hide behind the single MFMA issued before them, so every slice
-            // would wait out the LDS latency.  Instead all fragments of step k+1 are
-            // read right after step k's barrier, while step k's MFMAs (on fragments
-            // read one step earlier) run.  MFMAs and a·X additions keep the order of
-            // the schedule below, so results are the same bits.
-            bf16x8 ar[4][SM], ac[4][SN], br[4][SM], bc[4][SN];
-            auto read_step = [&](int sl, bf16x8 (&r)[4][SM], bf16x8 (&c)[4][SN]) {
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk) load_frags(sl, kk, r[kk], c[kk]);
-            };
-            auto step = [&](int k, const bf16x8 (&r)[4][SM], const bf16x8 (&c)[4][SN],
-                            bf16x8 (&nr)[4][SM], bf16x8 (&nc)[4][SN]) {
-                const int next = slot + 1 == kStages ? 0 : slot + 1;
-                // the same waits as the schedule below: panel k+1, before this
-                // step's DMA group
-                const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
-                if (kEpiPrefetch && k > nkl - kStages)
-                    wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
-                else
-                    wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
-                read_step(next, nr, nc);  // stale on the last step, not used
-                __builtin_amdgcn_sched_barrier(0);
-                constexpr int kM = 4 * kMfmaPerSlice;
-                const int dstep = kbeg + k + kStages;
-                const bool live = k + kStages < nkl;
-#pragma unroll
-                for (int m = 0; m < kM; ++m) {
-                    const int kk = m / kMfmaPerSlice, ij = m % kMfmaPerSlice;
-                    acc[ij / SN][ij % SN] =
-                        mfma_32x32x16(c[kk][ij % SN], r[kk][ij / SN], acc[ij / SN][ij % SN]);
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int d = m * Geo::kLoads / kM; d < (m + 1) * Geo::kLoads / kM; ++d)
-                        dma_one(d, dstep, slot, live);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                if constexpr (kAxInLoop) {
-                    if (k + 1 < nkl) add_ax(next, kbeg + k + 1);
-                }
-                if constexpr (kEpiPrefetch) {
-                    if (k == nkl - kStages) issue_epi(epi_slot);
-                }
-                slot = next;
-            };
-            if constexpr (kAxInLoop) add_ax(0, kbeg);
-            read_step(0, ar, ac);
-            int k = 0;
-            for (; k + 1 < nkl; k += 2) {
-                step(k, ar, ac, br, bc);
-                step(k + 1, br, bc, ar, ac);
-            }
-            if (k < nkl) step(k, ar, ac, br, bc);
-        } else {
-            bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
-            load_frags(0, 0, fr0, fc0);
-            for (int k = 0; k < nkl; ++k) {
-                const int next = slot + 1 == kStages ? 0 : slot + 1;
-                if constexpr (kAxInLoop) add_ax(slot, kbeg + k);
-                load_frags(slot, 1, fr1, fc1);
-                mfmas(fr0, fc0);
-                for (int z = 0; z < kMfmaPerSlice; ++z) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                load_frags(slot, 2, fr0, fc0);
-                mfmas(fr1, fc1);
-                for (int z = 0; z < kMfmaPerSlice; ++z) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                load_frags(slot, 3, fr1, fc1);
-                mfmas(fr0, fc0);
-                for (int z = 0; z < kMfmaPerSlice; ++z) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                // Wait for panel k+1.  The DMA groups issued after it (each step issues
-                // one, to the ring or the sink; the prologue issued npro) may stay in
-                // flight: prologue panels k+2 .. npro-1 and the groups of steps
-                // k+2-kStages .. k-1, at most kStages-2 groups (plus the epilogue tile
-                // once issued).  Unconditional, also on the last step (nothing needed is
-                // in flight then, and the fragments read from the stale slot are not
-                // used): a branch around these LDS reads makes the compiler's wait
-                // counts on the join below assume none were issued, and the slice-3
-                // MFMAs would then wait for all of them.
-                const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
-                if (kEpiPrefetch && k > nkl - kStages)
-                    wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
-                else
-                    wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
-                mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
-                                     fc0);
-                __builtin_amdgcn_sched_barrier(0);
-                if constexpr (kEpiPrefetch) {
-                    if (k == nkl - kStages) issue_epi(epi_slot);
-                }
-                slot = next;
-            }
-        }
-        // All waves are done with the ring (and no DMA is outstanding).
-        wait_vm_barrier<0>();
-
-        // -------------------------------------------------------- stream-K fixup
-        bool epi_issued = false;
-        if (kbeg != 0 || kend != nk) {
-            // This tile is cut between units u0 .. u1.  Each contributor but the
-            // last stores its fp32 partial and counts itself in; the last one to
-            // arrive forms p(u1) + p(u1 - 1) + ... + p(u0) in that fixed order (so
-            // results do not depend on arrival order) and runs the epilogue.
-            const int u0 = sk_unit_of(g, tstart), u1 = sk_unit_of(g, tstart + nk - 1);
-            const uint32_t others = static_cast<uint32_t>(u1 - u0);
-            uint64_t *cnt = g.counters + lt;
-            const uint64_t tok = uint64_t(g.token) << 32;
-            auto count_of = [&](uint64_t w) -> uint32_t {
-                return (w & 0xffffffff00000000ull) == tok ? static_cast<uint32_t>(w) : 0u;
-            };
-            // Partials and counters are accessed device-coherently (sc1 stores and
-            // loads, agent-scope atomics), so no whole-cache write-back or
-            // invalidate is needed: a contributor's stores are complete before its
-            // count is added, and the last contributor reads them after seeing
-            // every count.  The L2 contents the other workgroups are streaming
-            // from stay intact.
-            constexpr int kSc1 = 16;  // cache-policy bits of a device-scope access
-            const int64_t slot_bytes = int64_t(BM) * BN * 4;
-            const __amdgpu_buffer_rsrc_t rs_part =
-                __builtin_amdgcn_make_buffer_rsrc(g.partials, 0, 0x7fffffff, 0x00020000);
-            auto lane_base = [&](int u) {
-                return static_cast<uint32_t>(int64_t(sk_slot(u, lt)) * slot_bytes) + tid * 16;
-            };
-            // Slot layout: 16-byte chunk c = (i * SN + j) * 4 + q of every thread,
-            // thread-minor, so each access instruction covers 1 KiB contiguously.
-            constexpr uint32_t kChunkStride = kThreads * 16;
-            auto store_own = [&]() {
-                const uint32_t base = lane_base(unit);
-#pragma unroll
-                for (int i = 0; i < SM; ++i)
-#pragma unroll
-                    for (int j = 0; j < SN; ++j)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            __builtin_amdgcn_raw_buffer_store_b128(
-                                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                                      acc[i][j][4 * q + 3]},
-                                rs_part, base + ((i * SN + j) * 4 + q) * kChunkStride, 0, kSc1);
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            };
-            if (tid == 0)
-                s_arrived = count_of(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-            __syncthreads();
-            bool last = __builtin_amdgcn_readfirstlane(s_arrived) == others;
-            bool stored = false;
-            if (!last) {
-                store_own();
-                stored = true;
-                __syncthreads();
-                if (tid == 0) {
-                    // count this unit in: compare-and-swap, starting from zero when the
-                    // word holds another launch's token (each failed exchange means
-                    // another contributor got in, so at most two retries)
-                    uint64_t old = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    uint32_t before = count_of(old);
-                    while (!__hip_atomic_compare_exchange_strong(
-                        cnt, &old, tok | (before + 1u), __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                        __HIP_MEMORY_SCOPE_AGENT))
-                        before = count_of(old);
-                    s_arrived = before;
-                }
-                __syncthreads();
-                last = __builtin_amdgcn_readfirstlane(s_arrived) == others;
-            }
-            if (!last) continue;
-            // Every other contributor has counted itself in: the word is this
-            // unit's alone now.  Leave a zero count under this launch's token (a
-            // replay of the launch reuses the token).
-            if (tid == 0) __hip_atomic_store(cnt, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            // The epilogue operand tile (poly's A tile, which fills the idle ring) is
-            // fetched now, so that its round trip overlaps the partials' reads
-            // instead of following them.
-            if constexpr (kEpiLoad && !kEpiPrefetch) {
-                issue_epi(0);
-                epi_issued = true;
-            }
-            // Own partial first or second in the order: add the others to it in
-            // place (x + y == y + x).  Further back: start from p(u1) in memory.
-            const bool from_memory = u1 - unit >= 2;
-            if (from_memory && !stored) store_own();  // read back by the same lanes
-            // Partials are read a row-block (16 chunks per lane) at a time, the
-            // next block's loads in flight while the current one is added.
-            auto add_partial = [&](int u, bool assign) {
-                const uint32_t base = lane_base(u);
-                // blocks of kBlk accumulator tiles (i, j), the next block's loads in
-                // flight while one is added (one row-block of SN tiles; one tile
-                // for the 256-register accumulators)
-                constexpr int kBlk = kBigAcc ? 1 : SN;
-                constexpr int kBlocks = SM * SN / kBlk;
-                f32x4 x[2][kBlk * 4];
-                auto load_block = [&](int blk, f32x4 (&dst)[kBlk * 4]) {
-#pragma unroll
-                    for (int c = 0; c < kBlk * 4; ++c)
-                        dst[c] = __builtin_amdgcn_raw_buffer_load_b128(
-                            rs_part, base + (blk * kBlk * 4 + c) * kChunkStride, 0, kSc1);
-                };
-                load_block(0, x[0]);
-#pragma unroll
-                for (int blk = 0; blk < kBlocks; ++blk) {
-                    if (blk + 1 < kBlocks) load_block(blk + 1, x[(blk + 1) & 1]);
-#pragma unroll
-                    for (int t = 0; t < kBlk; ++t) {
-                        const int ij = blk * kBlk + t, i = ij / SN, j = ij % SN;
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                acc[i][j][4 * q + e] = assign ? x[blk & 1][t * 4 + q][e]
-                                                              : acc[i][j][4 * q + e] +
-                                                                    x[blk & 1][t * 4 + q][e];
-                    }
-                }
-            };
-            if (from_memory) add_partial(u1, true);
-            for (int u = from_memory ? u1 - 1 : u1; u >= u0; --u)
-                if (from_memory || u != unit) add_partial(u, false);
-        }
-
-        // -------------------------------------------------------- epilogue
-        uint16_t *tile = smem + epi_slot * (Geo::kStageBytes / 2);
-        uint16_t *out = g.out + bt * g.sb_out;
-        const bool diag = Tr::kSymmetric && (tm == tn);
-
-        if constexpr (kEpiLoad && !kEpiPrefetch) {
-            if (!epi_issued) issue_epi(0);
-            wait_vm_barrier<0>();
-        }
-
-        // Each lane turns its accumulators into bf16 results in place.
-#pragma unroll
-        for (int i = 0; i < SM; ++i) {
-            const int r = wr * WM + i * 32 + (lane & 31);
-#pragma unroll
-            for (int j = 0; j < SN; ++j) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
-                    u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
-                    float e[4] = {0.f, 0.f, 0.f, 0.f};
-                    uint16_t h[4];
-                    if constexpr (kAxInLoop) {
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) h[t] = f32_to_bf16_bits(acc[i][j][4 * q + t]);
-                    } else {
-                        if constexpr (kEpiLoad) unpack4(*p, e);
-                        epilogue_values<S>(acc[i][j], q, e, g, h);
-                    }
-                    *p = pack4(h);
-                }
-            }
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-
-        // Coalesced store of the tile: 16-byte chunks, consecutive threads along a row.
-        constexpr int kChunksPerRow = BN / 8;
-        for (int idx = tid; idx < BM * kChunksPerRow; idx += kThreads) {
-            const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
-            const int gr = row0 + row, gc = col0 + 8 * c;
-            if constexpr (!Tr::kSymmetric) {
-                if (gr >= g.out_rows || gc >= g.out_cols) continue;
-            }
-            u32x4 v;
-            if (!diag) {
-                v = *reinterpret_cast<const u32x4 *>(tile + epi_offset<BN>(row, 8 * c));
-            } else {
-                // Diagonal tile: element (r, c) comes from the upper-triangle source
-                // min/max(r, c), so the stored matrix is bitwise symmetric.
-                uint32_t hh[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int col = 8 * c + e;
-                    hh[e] = row <= col ? tile[epi_offset<BN>(row, col)]
-                                       : tile[epi_offset<BN>(col, row)];
-                }
-                v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
-                          hh[6] | (hh[7] << 16)};
-            }
-            if (Tr::kSymmetric) {
-                *reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc) = v;
-            } else if (g.out_vec) {
-                // Y is not read again by this step: a non-temporal store keeps it from
-                // displacing operand panels in L2 ([8,512,2048] 46.8 -> 44.4 us; the
-                // large shapes unchanged; A and P, read by the next stage, stay cached)
-                __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + gr * g.ld_out + gc));
-            } else {
-                // rows of n % 8 != 0 elements: 2-byte stores up to the last column
-                uint16_t *dst = out + gr * g.ld_out + gc;
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (gc + e < g.out_cols) dst[e] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
-            }
-        }
-
-        // Mirrored store (symmetric stages, off-diagonal tiles): row c of the
-        // mirror tile is column c of this tile; consecutive threads walk along it.
-        if constexpr (Tr::kSymmetric) {
-            if (!diag) {
-                constexpr int kMirrorChunks = BM / 8;  // 16-byte chunks per mirror row
-                for (int idx = tid; idx < BN * kMirrorChunks; idx += kThreads) {
-                    const int mc = idx / kMirrorChunks, rb = idx % kMirrorChunks;
-                    uint32_t hh[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) hh[e] = tile[epi_offset<BN>(8 * rb + e, mc)];
-                    const u32x4 v{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16),
-                                  hh[4] | (hh[5] << 16), hh[6] | (hh[7] << 16)};
-                    *reinterpret_cast<u32x4 *>(out + (col0 + mc) * g.ld_out + row0 + 8 * rb) = v;
-                }
-            }
-        }
+        stream_segment<BM, BN, S, NW, D>(g, smem, sink, &s_arrived, unit, tile_base, lt, kbeg,
+                                         kend);
     }
 }
 
