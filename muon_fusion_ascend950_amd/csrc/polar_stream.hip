@@ -778,14 +778,16 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
 }
 
 // Instantiated (tile, waves, depth) combinations: 256x256 with 8 or 4 waves and
-// two slots; smaller tiles with 4 waves and the depths their LDS allows
-// (128x128: 2 or 4 slots of 32 KiB; 64x64: 2, 4 or 8 of 16 KiB; 128x256 and
-// 256x128: 2 or 3 of 48 KiB; 192x192: 2).
+// two slots; 128x128 with 8 or 4 waves and 2 or 4 slots of 32 KiB (8 waves: two
+// per SIMD, 64x32 wave tiles; [16,512,2048] 62.5 -> 59.0 us, [1,1024,4096]
+// 46.3 -> 43.9 us against 4 waves); other tiles with 4 waves and the depths their
+// LDS allows (64x64: 2, 4 or 8 of 16 KiB; 128x256 and 256x128: 2 or 3 of 48 KiB;
+// 192x192: 2).
 template <int BM, int BN>
 constexpr bool depth_ok(int waves, int depth) {
     if (BM == 256 && BN == 256) return depth == 2 && (waves == 8 || waves == 4);
+    if (BM == 128 && BN == 128) return (waves == 4 || waves == 8) && (depth == 2 || depth == 4);
     if (waves != 4) return false;
-    if (BM == 128 && BN == 128) return depth == 2 || depth == 4;
     if (BM == 64 && BN == 64) return depth == 2 || depth == 4 || depth == 8;
     if (BM != BN) return depth == 2 || depth == 3;
     return depth == 2;
@@ -803,6 +805,7 @@ const void *kernel_for(int waves, int depth) {
     if constexpr (BM == 256 && BN == 256) {
         return waves == 8 ? kernel_ptr<BM, BN, S, 8, 2>() : kernel_ptr<BM, BN, S, 4, 2>();
     } else if constexpr (BM == 128 && BN == 128) {
+        if (waves == 8) return depth == 4 ? kernel_ptr<BM, BN, S, 8, 4>() : kernel_ptr<BM, BN, S, 8, 2>();
         return depth == 4 ? kernel_ptr<BM, BN, S, 4, 4>() : kernel_ptr<BM, BN, S, 4, 2>();
     } else if constexpr (BM == 64 && BN == 64) {
         return depth == 8   ? kernel_ptr<BM, BN, S, 4, 8>()
@@ -849,7 +852,7 @@ const void *stream_kernel(Stage s, int bm, int bn, int waves, int depth) {
 }  // namespace
 
 int stream_waves(int bm, int bn, int requested) {
-    return (bm == 256 && bn == 256 && requested == 8) ? 8 : 4;
+    return (((bm == 256 && bn == 256) || (bm == 128 && bn == 128)) && requested == 8) ? 8 : 4;
 }
 
 bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth) {

@@ -372,6 +372,11 @@ def test_noncontiguous_input():
     {"MUON_POLAR_APPLY_TILE_M": "128", "MUON_POLAR_APPLY_TILE_N": "256"},
     {"MUON_POLAR_GRAM_TILE": "192", "MUON_POLAR_POLY_TILE": "192"},
     {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_APPLY_TILE_M": "256", "MUON_POLAR_WAVES": "8"},
+    {"MUON_POLAR_GRAM_TILE": "128", "MUON_POLAR_POLY_TILE": "128", "MUON_POLAR_APPLY_TILE_M": "128",
+     "MUON_POLAR_WAVES": "4"},
+    {"MUON_POLAR_GRAM_TILE": "128", "MUON_POLAR_POLY_TILE": "128", "MUON_POLAR_APPLY_TILE_M": "128",
+     "MUON_POLAR_WAVES": "8", "MUON_POLAR_GRAM_DEPTH": "4", "MUON_POLAR_POLY_DEPTH": "4",
+     "MUON_POLAR_APPLY_DEPTH": "4"},
     {"MUON_POLAR_GRAM_TILE": "192", "MUON_POLAR_POLY_TILE": "256"},
     {"MUON_POLAR_GRAM_TILE": "128", "MUON_POLAR_POLY_TILE": "192", "MUON_POLAR_APPLY_TILE_M": "256",
      "MUON_POLAR_APPLY_TILE_N": "128"},
