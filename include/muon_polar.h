@@ -30,12 +30,13 @@
  * workspace needs no clearing (any content, graph replays included).  Calls that
  * share one workspace must not overlap (use one workspace per concurrent stream).
  *
- * Rows of n % 64 != 0 elements: each step first copies X into a zero-padded
+ * Rows of n % 8 != 0 elements: each step first copies X into a zero-padded
  * [batch, m, roundup(n, 64)] buffer at the end of the workspace, so that the
- * DMA-fed kernels (16-byte global->LDS transfers of whole 64-element K-steps)
- * serve every width; Y is written at its own width (2-byte stores when
- * n % 8 != 0).  Shapes whose padded copy would reach 2^30 elements per matrix
- * are rejected ("matrix too large"), like X itself.
+ * DMA-fed kernels (16-byte global->LDS transfers) serve every width; Y is
+ * written at its own width (2-byte stores).  Rows of n % 8 == 0 elements are
+ * read in place, the chunks of a last K-step past n masked to zeros (the same
+ * sums as the padded copy, bit for bit).  Shapes whose padded copy would reach
+ * 2^30 elements per matrix are rejected ("matrix too large"), like X itself.
  *
  * Buffers: x, y and the workspace must be pairwise disjoint (no in-place call:
  * every output tile of stage 3 reads X's whole K range while other tiles are
@@ -116,7 +117,7 @@ int muon_polar_step_noalloc(const void *x, void *y, int64_t batch, int64_t m, in
  * ignored: the stage runs one output tile per workgroup) or a buffer of
  * info.workspace_bytes, the same one muon_polar_step takes (gram / poly may be
  * its A / P areas), which lets the stage use the stream-K split (and, for
- * n % 64 != 0, the padded copy of X) exactly as inside muon_polar_step, so the
+ * n % 8 != 0, the padded copy of X) exactly as inside muon_polar_step, so the
  * three calls reproduce the step bit for bit.  The reference's stage launchers
  * likewise take a device-side buffer (their tiling struct).  The stages take
  * m <= n only. */

@@ -129,10 +129,11 @@ struct Plan {
     bool sk_any;
     int64_t counter_stride;
     size_t counters_offset, partials_offset;
-    // n % 64 != 0: each step first copies X into a zero-padded [batch, m, np]
+    // n % 8 != 0: each step first copies X into a zero-padded [batch, m, np]
     // buffer (np = roundup(n, 64)) at pad_offset, which the DMA-fed kernels read
-    // (their K-contiguous panels need rows of whole 64-element K-steps: they apply
-    // no K masks); Y is stored at its own width (2-byte stores for n % 8 != 0).
+    // (their panels are 16-byte chunks, which rows of n % 8 != 0 elements do not
+    // align to); Y is stored at its own width (2-byte stores).  Rows of
+    // n % 8 == 0 elements are read in place, a last K-step past n masked.
     bool pad;
     int64_t np;
     size_t pad_offset;
@@ -331,7 +332,7 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "grid too large");
 
     const int cus = tgt.cus;
-    p.pad = p.stream && n % 64 != 0;
+    p.pad = p.stream && n % 8 != 0;
     p.np = p.pad ? round_up(n, 64) : n;
     // the padded copy of X is read with the same 32-bit offsets as X
     if (m * p.np >= kMaxMatrixElems)
@@ -513,6 +514,9 @@ struct StageLaunch {
     // byte extent of one batch matrix of rowop, colop and epi, in 64 bits (the
     // GemmArgs fields are 32-bit)
     int64_t extent[3];
+    // X rows read in place end inside the last K-step (ldx % 64 != 0): the
+    // kernel masks that step's chunks past row_k (gram and apply-right)
+    bool k_tail;
     GemmArgs g;
 };
 
@@ -539,8 +543,10 @@ StageLaunch gram_launch(const Plan &p, const void *x, int64_t ldx, void *gram, i
     L.extent[0] = L.extent[1] = L.extent[2] = m * ldx * 2;
     g.group_n = sym_group();
     const bool vec = (ldx % 8 == 0) && aligned16(x);
-    // DMA-fed: X rows are K-contiguous panels, read in whole 64-element K-steps
-    const bool dma = vec && ldx % 64 == 0;
+    // DMA-fed: X rows are K-contiguous panels of 16-byte chunks; a last K-step
+    // past n (ldx % 64 != 0) is loaded with its chunks past n masked
+    const bool dma = vec;
+    L.k_tail = ldx % 64 != 0;
     L.stage = Stage::Gram;
     L.sk_index = 0;
     L.bm = L.bn = p.gram_tile;
@@ -690,6 +696,7 @@ StageLaunch apply_r_launch(const Plan &p, const void *poly, const void *x, int64
     L.extent[1] = p.mp * p.mp * 2;
     g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : 0;
     g.group_n = apply_group(p);
+    L.k_tail = ldx % 64 != 0;
     L.stage = Stage::ApplyR;
     L.sk_index = 2;
     L.bm = p.apply_bm;
@@ -733,7 +740,8 @@ int launch_stage(StageLaunch &L, int64_t batch, const Plan &p, const SkArea *are
     prepare_stage(L, batch, p, area, g_launch_token.fetch_add(1, std::memory_order_relaxed));
     const hipError_t e =
         L.stream_ok
-            ? muon_polar::launch_stream(L.stage, L.bm, L.bn, L.waves, L.depth, L.g, stream)
+            ? muon_polar::launch_stream(L.stage, L.bm, L.bn, L.waves, L.depth, L.g, stream,
+                                        L.k_tail)
             : muon_polar::launch_gemm(L.stage, L.bm, L.bn, L.vec, L.g, static_cast<int>(L.grid),
                                       stream);
     return finish_stage(e, stream, name);

@@ -82,9 +82,12 @@ hipError_t launch_gemm(Stage s, int bm, int bn, bool vec, const GemmArgs &g, int
 // DMA-fed kernels: X chunks of 16 B must be entirely inside or outside the matrix
 // (n % 8 == 0, 16-byte aligned X).  Grid is g.sk_units + 8 * g.per_xcd; `waves`
 // per workgroup as returned by stream_waves; `depth` LDS ring slots (one K-step
-// each), a combination stream_depth_supported accepts.
+// each), a combination stream_depth_supported accepts.  k_mask (gram and
+// apply-right only): the K-contiguous operands' rows end inside the last K-step
+// (X rows of n % 64 != 0 elements read in place), so the K-masked variant loads
+// that step's chunks past row_k / col_k as zeros.
 hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const GemmArgs &g,
-                         hipStream_t stream);
+                         hipStream_t stream, bool k_mask = false);
 
 // Whether a DMA-fed kernel exists for (s, bm, bn, waves, depth).
 bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth);

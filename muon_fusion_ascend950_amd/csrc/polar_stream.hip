@@ -105,7 +105,7 @@ __device__ __forceinline__ int epi_offset(int row, int col) {
 // tile_base + lt (its stream-K fixup when the tile is cut, and its epilogue when
 // this workgroup completes it).  `smem`, `sink` and `s_arrived` are the caller's
 // LDS: the ring of D K-step slots, the per-wave DMA sink and one arrival word.
-template <int BM, int BN, Stage S, int NW, int D>
+template <int BM, int BN, Stage S, int NW, int D, bool KT>
 __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem, uint16_t *sink,
                                                uint32_t *s_arrived_p, int unit, int tile_base,
                                                int lt, int kbeg, int kend) {
@@ -230,15 +230,25 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // (An idle instruction whose row is outside the matrix wraps to offset 0:
     // an in-range read, also into the sink.)
     const uint32_t sink_base = lds_addr(sink) + wave * 1024;
+    // KT (gram and apply-right reading X rows of n % 64 != 0, n % 8 == 0
+    // elements in place): chunks at K positions past the operand's K extent
+    // (row_k, col_k; only in the last K-step) take an out-of-range offset, so
+    // they read the zeros a padded copy of X would hold there, and the sums are
+    // the padded copy's bit for bit.
+    static_assert(!KT || (!Tr::kRowNC && !Tr::kColNC), "K masks of K-contiguous panels");
     auto dma_one = [&](int d, int step, int slot, bool live) {
         const int k0 = step * kBK;
         if (d < Geo::kLoadsA) {
             const uint32_t koff = live ? a_step(k0) : kOob;
-            dma_16B(rs_row, live ? a_dst(slot, d) : sink_base, off_a[d] + koff);
+            uint32_t off = off_a[d] + koff;
+            if constexpr (KT) off = k0 + 8 * a_chunk(d) < g.row_k ? off : kOob;
+            dma_16B(rs_row, live ? a_dst(slot, d) : sink_base, off);
         } else {
             const int i = d - Geo::kLoadsA;
             const uint32_t koff = live ? b_step(k0) : kOob;
-            dma_16B(rs_col, live ? b_dst(slot, i) : sink_base, off_b[i] + koff);
+            uint32_t off = off_b[i] + koff;
+            if constexpr (KT) off = k0 + 8 * b_chunk(i) < g.col_k ? off : kOob;
+            dma_16B(rs_col, live ? b_dst(slot, i) : sink_base, off);
         }
     };
     auto issue_all = [&](int step, int slot) {
@@ -742,7 +752,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     }
 }
 
-template <int BM, int BN, Stage S, int NW, int D>
+template <int BM, int BN, Stage S, int NW, int D, bool KT>
 __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     using Geo = StreamGeom<BM, BN, NW, D>;
     constexpr int kStages = Geo::kStages;
@@ -772,7 +782,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         const int kbeg = static_cast<int>(lo - tstart), kend = static_cast<int>(hi - tstart);
         if (hi != it_hi) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         hi = lo;
-        stream_segment<BM, BN, S, NW, D>(g, smem, sink, &s_arrived, unit, tile_base, lt, kbeg,
+        stream_segment<BM, BN, S, NW, D, KT>(g, smem, sink, &s_arrived, unit, tile_base, lt, kbeg,
                                          kend);
     }
 }
@@ -793,58 +803,62 @@ constexpr bool depth_ok(int waves, int depth) {
     return depth == 2;
 }
 
-template <int BM, int BN, Stage S, int NW, int D>
+template <int BM, int BN, Stage S, int NW, int D, bool KT>
 const void *kernel_ptr() {
-    return reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, NW, D>);
+    return reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, NW, D, KT>);
 }
 
-// Kernel of (BM, BN, S) for the given waves and depth, or null.
-template <int BM, int BN, Stage S>
+// Kernel of (BM, BN, S, KT) for the given waves and depth, or null.
+template <int BM, int BN, Stage S, bool KT>
 const void *kernel_for(int waves, int depth) {
     if (!depth_ok<BM, BN>(waves, depth)) return nullptr;
     if constexpr (BM == 256 && BN == 256) {
-        return waves == 8 ? kernel_ptr<BM, BN, S, 8, 2>() : kernel_ptr<BM, BN, S, 4, 2>();
+        return waves == 8 ? kernel_ptr<BM, BN, S, 8, 2, KT>() : kernel_ptr<BM, BN, S, 4, 2, KT>();
     } else if constexpr (BM == 128 && BN == 128) {
-        if (waves == 8) return depth == 4 ? kernel_ptr<BM, BN, S, 8, 4>() : kernel_ptr<BM, BN, S, 8, 2>();
-        return depth == 4 ? kernel_ptr<BM, BN, S, 4, 4>() : kernel_ptr<BM, BN, S, 4, 2>();
+        if (waves == 8)
+            return depth == 4 ? kernel_ptr<BM, BN, S, 8, 4, KT>() : kernel_ptr<BM, BN, S, 8, 2, KT>();
+        return depth == 4 ? kernel_ptr<BM, BN, S, 4, 4, KT>() : kernel_ptr<BM, BN, S, 4, 2, KT>();
     } else if constexpr (BM == 64 && BN == 64) {
-        return depth == 8   ? kernel_ptr<BM, BN, S, 4, 8>()
-               : depth == 4 ? kernel_ptr<BM, BN, S, 4, 4>()
-                            : kernel_ptr<BM, BN, S, 4, 2>();
+        return depth == 8   ? kernel_ptr<BM, BN, S, 4, 8, KT>()
+               : depth == 4 ? kernel_ptr<BM, BN, S, 4, 4, KT>()
+                            : kernel_ptr<BM, BN, S, 4, 2, KT>();
     } else if constexpr (BM != BN) {
-        return depth == 3 ? kernel_ptr<BM, BN, S, 4, 3>() : kernel_ptr<BM, BN, S, 4, 2>();
+        return depth == 3 ? kernel_ptr<BM, BN, S, 4, 3, KT>() : kernel_ptr<BM, BN, S, 4, 2, KT>();
     } else {
-        return kernel_ptr<BM, BN, S, 4, 2>();
+        return kernel_ptr<BM, BN, S, 4, 2, KT>();
     }
 }
 
-template <Stage S>
+template <Stage S, bool KT>
 const void *kernel_by_tile(int bm, int bn, int waves, int depth) {
-    if (bm == 64 && bn == 64) return kernel_for<64, 64, S>(waves, depth);
-    if (bm == 128 && bn == 128) return kernel_for<128, 128, S>(waves, depth);
-    if (bm == 256 && bn == 256) return kernel_for<256, 256, S>(waves, depth);
+    if (bm == 64 && bn == 64) return kernel_for<64, 64, S, KT>(waves, depth);
+    if (bm == 128 && bn == 128) return kernel_for<128, 128, S, KT>(waves, depth);
+    if (bm == 256 && bn == 256) return kernel_for<256, 256, S, KT>(waves, depth);
     if constexpr (S == Stage::Gram || S == Stage::Poly) {
-        if (bm == 192 && bn == 192) return kernel_for<192, 192, S>(waves, depth);
+        if (bm == 192 && bn == 192) return kernel_for<192, 192, S, KT>(waves, depth);
     }
     if constexpr (!StageTraits<S>::kSymmetric) {
-        if (bm == 128 && bn == 256) return kernel_for<128, 256, S>(waves, depth);
-        if (bm == 256 && bn == 128) return kernel_for<256, 128, S>(waves, depth);
+        if (bm == 128 && bn == 256) return kernel_for<128, 256, S, KT>(waves, depth);
+        if (bm == 256 && bn == 128) return kernel_for<256, 128, S, KT>(waves, depth);
     }
     return nullptr;
 }
 
-const void *stream_kernel(Stage s, int bm, int bn, int waves, int depth) {
+// kt: the K-masked variant (gram and apply-right only).
+const void *stream_kernel(Stage s, int bm, int bn, int waves, int depth, bool kt) {
     switch (s) {
         case Stage::Gram:
-            return kernel_by_tile<Stage::Gram>(bm, bn, waves, depth);
+            return kt ? kernel_by_tile<Stage::Gram, true>(bm, bn, waves, depth)
+                      : kernel_by_tile<Stage::Gram, false>(bm, bn, waves, depth);
         case Stage::Poly:
-            return kernel_by_tile<Stage::Poly>(bm, bn, waves, depth);
+            return kt ? nullptr : kernel_by_tile<Stage::Poly, false>(bm, bn, waves, depth);
         case Stage::Apply:
-            return kernel_by_tile<Stage::Apply>(bm, bn, waves, depth);
+            return kt ? nullptr : kernel_by_tile<Stage::Apply, false>(bm, bn, waves, depth);
         case Stage::GramT:
-            return kernel_by_tile<Stage::GramT>(bm, bn, waves, depth);
+            return kt ? nullptr : kernel_by_tile<Stage::GramT, false>(bm, bn, waves, depth);
         case Stage::ApplyR:
-            return kernel_by_tile<Stage::ApplyR>(bm, bn, waves, depth);
+            return kt ? kernel_by_tile<Stage::ApplyR, true>(bm, bn, waves, depth)
+                      : kernel_by_tile<Stage::ApplyR, false>(bm, bn, waves, depth);
     }
     return nullptr;
 }
@@ -856,12 +870,12 @@ int stream_waves(int bm, int bn, int requested) {
 }
 
 bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth) {
-    return stream_kernel(s, bm, bn, waves, depth) != nullptr;
+    return stream_kernel(s, bm, bn, waves, depth, false) != nullptr;
 }
 
 hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const GemmArgs &g,
-                         hipStream_t stream) {
-    const void *k = stream_kernel(s, bm, bn, waves, depth);
+                         hipStream_t stream, bool k_mask) {
+    const void *k = stream_kernel(s, bm, bn, waves, depth, k_mask);
     if (k == nullptr) return hipErrorInvalidValue;
     const int grid = g.sk_units + 8 * g.per_xcd;
     GemmArgs copy = g;
@@ -870,7 +884,7 @@ hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const Ge
 }
 
 int stream_blocks_per_cu(Stage s, int bm, int bn, int waves, int depth) {
-    const void *k = stream_kernel(s, bm, bn, waves, depth);
+    const void *k = stream_kernel(s, bm, bn, waves, depth, false);
     if (k == nullptr) return 0;
     int n = 0;
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 64 * waves, 0) == hipSuccess ? n

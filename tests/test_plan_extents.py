@@ -95,11 +95,23 @@ def test_without_a_device_count_nothing_splits():
     assert all(plan.stage[s].sk_units == 0 for s in range(3))
 
 
-@pytest.mark.parametrize("shape", [(1, 32512, 33025), (1, 10_000_000, 72), (1, 20_000_000, 8)])
+@pytest.mark.parametrize("shape", [(1, 32512, 33025), (1, 16_000_000, 66), (1, 4_000_000, 260)])
 def test_padded_copy_beyond_32_bit_offsets_is_rejected(shape):
-    """X fits 32-bit offsets but its copy padded to a multiple of 64 columns would
-    not (2.15-2.56 GB): the out-of-range marker of the DMA (offset 2^31) would then
-    address real rows.  Such shapes are rejected."""
+    """Rows of n % 8 != 0 elements go through a copy padded to a multiple of 64
+    columns.  X fits 32-bit offsets here but that copy would not (2.15-2.56 GB): the
+    out-of-range marker of the DMA (offset 2^31) would then address real rows.  Such
+    shapes are rejected."""
     with pytest.raises(capi.CapiError, match="too large") as err:
         capi.query(*shape)
     assert err.value.status == capi.ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("shape", [(1, 10_000_000, 72), (1, 20_000_000, 8), (2, 300, 1000),
+                                   (1, 1000, 3000), (3, 523, 200)])
+def test_rows_of_whole_chunks_are_read_in_place(shape):
+    """n % 8 == 0: X is read in place (a last K-step past n is masked in the
+    kernels), so the plan holds no padded copy and such tall shapes, whose copy
+    padded to 64 columns would pass 2^30 elements, are accepted."""
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(1, 1, 1))
+    assert plan.pad_end == 0
+    check(plan)

@@ -321,6 +321,50 @@ def test_masking_equals_zero_padding(monkeypatch, shape):
     assert torch.equal(ys, yps)
 
 
+@pytest.mark.parametrize("shape", [(2, 300, 1000), (1, 2000, 4040), (1, 800, 8008), (3, 200, 136),
+                                   (2, 40, 56), (1, 8, 8)])
+@pytest.mark.parametrize("split", ["1", "0"])
+def test_rows_read_in_place_equal_a_zero_padded_copy(monkeypatch, shape, split):
+    """n % 8 == 0, n % 64 != 0: gram reads X in place and masks the chunks of its
+    last K-step past n (no padded copy).  A zero-padded input of roundup(n, 64)
+    columns has the same tiles and K-steps, so the same plan (split or not): Y must
+    equal its first n columns bit for bit.  Shapes: unsplit, split 128x128 and 64x64
+    gram (with stream-K segments that hold the last K-step alone), n < 64 (the only
+    K-step masked), m > n's wrapper excluded (m <= n here)."""
+    monkeypatch.setenv("MUON_POLAR_STREAM_K", split)
+    batch, m, n = shape
+    xc = O.make_input(shape, seed=31)
+    x = xc.to(DEV)
+    np_ = -(-n // 64) * 64
+    padded = torch.zeros(batch, m, np_, dtype=torch.bfloat16, device=DEV)
+    padded[:, :, :n] = x
+    y = polar_step(x, *C0)
+    yp = polar_step(padded, *C0)[:, :, :n]
+    torch.cuda.synchronize()
+    print(f"in-place rows {shape} split={split}", flush=True)
+    assert torch.equal(y, yp)
+    assert_matches_oracle(y, xc, [C0], 1e-2)
+
+
+@pytest.mark.parametrize("shape", [(3, 700, 200), (1, 4100, 1000), (2, 130, 72)])
+def test_tall_rows_read_in_place_equal_a_zero_padded_copy(monkeypatch, shape):
+    """m > n, n % 8 == 0, n % 64 != 0: apply-right reads X rows in place with the
+    last K-step masked; against X padded with zero columns to roundup(n, 64)
+    (unsplit: padding changes the Gram's tile count, and unsplit results do not
+    depend on the tiling), Y's first n columns are equal bit for bit."""
+    monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
+    batch, m, n = shape
+    x = O.make_input(shape, seed=32).to(DEV)
+    np_ = -(-n // 64) * 64
+    padded = torch.zeros(batch, m, np_, dtype=torch.bfloat16, device=DEV)
+    padded[:, :, :n] = x
+    y = polar_step(x, *C0)
+    yp = polar_step(padded, *C0)[:, :, :n]
+    torch.cuda.synchronize()
+    print(f"in-place tall rows {shape}", flush=True)
+    assert torch.equal(y, yp)
+
+
 @pytest.mark.parametrize("shape", [(130, 129), (2, 700, 300), (2050, 150)])
 def test_wrapper_transpose_is_exact(shape):
     x = O.make_input(shape, seed=8).to(DEV)
