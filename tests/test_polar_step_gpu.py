@@ -322,7 +322,8 @@ def test_masking_equals_zero_padding(monkeypatch, shape):
 
 
 @pytest.mark.parametrize("shape", [(2, 300, 1000), (1, 2000, 4040), (1, 800, 8008), (3, 200, 136),
-                                   (2, 40, 56), (1, 8, 8)])
+                                   (2, 40, 56), (1, 8, 8), (1, 129, 130), (2, 150, 2050),
+                                   (3, 100, 1002), (1, 1000, 3002), (2, 40, 58)])
 @pytest.mark.parametrize("split", ["1", "0"])
 def test_rows_read_in_place_equal_a_zero_padded_copy(monkeypatch, shape, split):
     """n % 8 == 0, n % 64 != 0: gram reads X in place and masks the chunks of its
@@ -330,7 +331,9 @@ def test_rows_read_in_place_equal_a_zero_padded_copy(monkeypatch, shape, split):
     columns has the same tiles and K-steps, so the same plan (split or not): Y must
     equal its first n columns bit for bit.  Shapes: unsplit, split 128x128 and 64x64
     gram (with stream-K segments that hold the last K-step alone), n < 64 (the only
-    K-step masked), m > n's wrapper excluded (m <= n here)."""
+    K-step masked); and rows of n % 8 != 0 elements (the odd-width BASELINE
+    configurations among them), which go through the step's own padded copy and
+    must give the same bits as the caller's; m <= n throughout."""
     monkeypatch.setenv("MUON_POLAR_STREAM_K", split)
     batch, m, n = shape
     xc = O.make_input(shape, seed=31)
