@@ -48,7 +48,8 @@ def raw_input(shape, seed, scale=3.0):
     return (torch.randn(shape, dtype=torch.bfloat16, generator=gen) * scale).to(DEV)
 
 
-@pytest.mark.parametrize("shape", [(8, 512, 2048), (2, 150, 2050), (3, 1024, 8192), (1, 4096, 14336)])
+@pytest.mark.parametrize("shape", [(8, 512, 2048), (2, 150, 2050), (3, 1024, 8192), (1, 4096, 14336),
+                                   (2, 300, 1000)])
 @pytest.mark.parametrize("k", [1, 2, 5])
 def test_steps_equal_chained_polar_step(shape, k):
     x = O.make_input(shape, seed=40).to(DEV)

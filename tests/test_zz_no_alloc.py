@@ -37,7 +37,7 @@ def test_noalloc_equals_workspace_entry(capi):
     # [4096,14336]: every stage cuts its last round (partials and arrival words in
     # the scratch); then smaller shapes over the scratch that call left behind
     for shape, seed in (((1, 4096, 14336), 0), ((8, 512, 2048), 1), ((2, 150, 2050), 2),
-                        ((1, 129, 130), 3)):
+                        ((1, 129, 130), 3), ((2, 300, 1000), 4)):
         print(f"noalloc {shape}", flush=True)
         x = O.make_input(shape, seed=seed).to(DEV)
         coeffs = O.COEFFICIENTS[seed % 5]
