@@ -16,10 +16,12 @@ Order of a run (rank 0, one GPU):
    would otherwise time that transient;
 2. the driver contract: W untimed warm-up calls, then exactly K timed calls between two
    device synchronisations → ``value``, ``ms_per_step``;
-3. per-stage device times (``kernel_us``): R back-to-back launches of one stage through
-   the C ABI, captured in a HIP graph and replayed between two HIP events on the launch
-   stream (no host gaps, no event fences between stages), with the step's workspace and
-   stream-K split; ``roofline`` uses stage 3 (P·X + a·X), the dominant kernel;
+3. per-stage device times inside a step (``kernel_us``): R repetitions of the step
+   (gram, poly, apply), of its tail (poly, apply) and of apply alone, launched through the
+   C ABI with the step's workspace and stream-K split, each captured in a HIP graph and
+   replayed between two HIP events on the launch stream (no host gaps); stage times are
+   the differences, so they sum to the replayed step (``graph_step_us``); ``roofline``
+   uses stage 3 (P·X + a·X), the dominant kernel;
 4. every BASELINE.json configuration with the reference's timing method (20 warm-ups,
    then the median of 5 repeats of 100 calls, README.md:179-191) after its accuracy gate
    (6e-2 against the fp32 formula, and relF = ‖Y − Y_fp32‖_F / ‖Y_fp32‖_F);
@@ -181,10 +183,14 @@ def settle(fn, seconds: float) -> int:
 
 
 def stage_times(batch: int, m: int, n: int, launches: int, repeats: int = 3) -> dict:
-    """µs per launch of each stage: `launches` back-to-back launches of one stage through
-    the C ABI (polar_step's workspace, A and P in it, the same stream-K split as inside
-    the step), captured in a HIP graph and replayed between two HIP events on the
-    capturing stream, the stream the kernels run on; the median of `repeats` replays."""
+    """µs per launch of each stage inside a step, from HIP-graph replays without host
+    gaps: `launches` repetitions of a stage sequence through the C ABI (polar_step's
+    workspace, A and P in it, the same stream-K split as inside the step) are captured
+    in one graph and replayed between two HIP events on the capturing stream (the
+    median of `repeats` replays).  Three sequences: the step (gram, poly, apply),
+    its tail (poly, apply) and apply alone.  apply = apply alone, poly = tail - apply,
+    gram = step - tail: each stage runs where it runs in a step (gram after an apply,
+    before a poly), and the three sum to the replayed step ("step")."""
     import torch
     from muon_fusion_ascend950_amd import capi
 
@@ -202,14 +208,16 @@ def stage_times(batch: int, m: int, n: int, launches: int, repeats: int = 3) -> 
     for name in STAGES:  # A and P in place before any stage is timed
         calls[name]()
     torch.cuda.synchronize()
-    out = {}
+    sequences = {"step": STAGES, "tail": STAGES[1:], "apply": STAGES[2:]}
+    per = {}
     stream = torch.cuda.Stream()
-    for name in STAGES:
+    for key, seq in sequences.items():
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
             with torch.cuda.graph(graph, stream=stream):
                 for _ in range(launches):
-                    calls[name]()
+                    for name in seq:
+                        calls[name]()
         graph.replay()  # warm-up replay
         torch.cuda.synchronize()
         samples = []
@@ -222,10 +230,11 @@ def stage_times(batch: int, m: int, n: int, launches: int, repeats: int = 3) -> 
                 stop.record()
             stop.synchronize()
             samples.append(start.elapsed_time(stop) * 1e3 / launches)
-        out[name] = statistics.median(samples)
+        per[key] = statistics.median(samples)
         del graph
     torch.cuda.synchronize()
-    return out
+    return {"gram": per["step"] - per["tail"], "poly": per["tail"] - per["apply"],
+            "apply": per["apply"], "step": per["step"]}
 
 
 # ----------------------------------------------------------------------------- comparison points
@@ -281,8 +290,9 @@ def run_metadata() -> dict:
         "tuning_variables": tuning or "defaults",
         "timing": ("value: settle, W warm-up calls, K calls between device synchronisations; "
                    "all_configs: 20 warm-ups, median of 5 x 100 calls (README.md:179-191); "
-                   "kernel_us: back-to-back launches of one stage, HIP-graph replay between "
-                   "HIP events on the launch stream"),
+                   "kernel_us: HIP-graph replays of R steps, R (poly, apply) and R apply "
+                   "between HIP events on the launch stream; stage times are their "
+                   "differences"),
     }
 
 
@@ -394,7 +404,8 @@ def main() -> int:
     ap.add_argument("--settle-s", type=float, default=1.0,
                     help="seconds of headline calls before the warm-up (GPU clock settling)")
     ap.add_argument("--stage-launches", type=int, default=50,
-                    help="back-to-back launches per stage in the graph-replayed stage timing")
+                    help="repetitions of each stage sequence (step, tail, apply) in the "
+                         "graph-replayed stage timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile", action="store_true",
                     help="only the headline phase (gate, settle, W + K steps), the stage "
@@ -471,8 +482,10 @@ def main() -> int:
         print(json.dumps({"profile": "polar_step [4096,14336] + stage loops", "steps": args.steps,
                           "warmup": args.warmup, "settle_calls": settled,
                           "us_per_step": round(sec * 1e6, 2),
-                          "kernel_us": {k: round(v, 2) for k, v in st.items()},
-                          "secondary_kernel_us": {k: round(v, 2) for k, v in st2.items()},
+                          "kernel_us": {k: round(st[k], 2) for k in STAGES},
+                          "graph_step_us": round(st["step"], 2),
+                          "secondary_kernel_us": {k: round(st2[k], 2) for k in STAGES},
+                          "secondary_graph_step_us": round(st2["step"], 2),
                           "stage_launches": [args.stage_launches, max(args.stage_launches, 100)],
                           "copy_bytes": 1 << 30}), flush=True)
         return 0
@@ -536,8 +549,9 @@ def main() -> int:
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
         "accuracy": gate,
         "settle": {"seconds": args.settle_s, "calls": settled},
-        "kernel_us": {k: round(v, 2) for k, v in st.items()},
-        "kernel_us_sum": round(sum(st.values()), 2),
+        "kernel_us": {k: round(st[k], 2) for k in STAGES},
+        "kernel_us_sum": round(sum(st[k] for k in STAGES), 2),
+        "graph_step_us": round(st["step"], 2),
         "torch_eager_us": round(eager * 1e6, 2),
         "speedup_vs_torch_eager": round(eager / sec, 3),
         "roofline": {
@@ -571,8 +585,9 @@ def main() -> int:
             "pct_bf16_peak": round(100 * fl2 / sec2 / 1e12 / PEAK_BF16_TFLOPS, 2),
             "pct_hbm_peak": round(100 * hbm2 / sec2 / 1e9 / PEAK_HBM_GBS, 2),
             "accuracy": gate2,
-            "kernel_us": {k: round(v, 2) for k, v in st2.items()},
-            "kernel_us_sum": round(sum(st2.values()), 2),
+            "kernel_us": {k: round(st2[k], 2) for k in STAGES},
+            "kernel_us_sum": round(sum(st2[k] for k in STAGES), 2),
+            "graph_step_us": round(st2["step"], 2),
             "torch_eager_us": round(eager2 * 1e6, 2),
             "speedup_vs_torch_eager": round(eager2 / sec2, 3),
         },
