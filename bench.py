@@ -168,6 +168,17 @@ def reference_method(fn, warmup: int = 20, calls: int = 100, repeats: int = 5) -
     return statistics.median(samples)
 
 
+def interleaved(fns, calls: int, warmup: int, rounds: int = 5) -> list:
+    """Seconds per call of each function, timed in alternation (`rounds` rounds of
+    `calls` calls each after `warmup` calls): the median per function, so that a drift
+    of the GPU clock affects the variants alike."""
+    samples = [[] for _ in fns]
+    for _ in range(rounds):
+        for i, fn in enumerate(fns):
+            samples[i].append(time_calls(fn, calls, warmup))
+    return [statistics.median(s) for s in samples]
+
+
 def settle(fn, seconds: float) -> int:
     """Run `fn` back to back for `seconds` (the GPU's clock settles under sustained load)."""
     import torch
@@ -510,8 +521,7 @@ def main() -> int:
         return y
 
     raw = raw.cuda()
-    sec_express = time_calls(lambda: mf.polar_express(raw), 10, 3)
-    sec_loop = time_calls(reference_loop, 10, 3)
+    sec_express, sec_loop = interleaved([lambda: mf.polar_express(raw), reference_loop], 10, 2)
 
     # Muon update of one fp32 [4096,14336] parameter: the native update (momentum pass,
     # normalisation, 5 steps, parameter update) vs nanochat's step in PyTorch eager
