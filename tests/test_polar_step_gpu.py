@@ -190,7 +190,8 @@ def _stages(x3: torch.Tensor, b: float, c: float):
     return gram, poly, mp
 
 
-@pytest.mark.parametrize("shape", [(2, 150, 2050), (1, 129, 130), (8, 512, 2048), (1, 300, 701)])
+@pytest.mark.parametrize("shape", [(2, 150, 2050), (1, 129, 130), (8, 512, 2048), (1, 300, 701),
+                                   (2, 300, 1000)])
 def test_stages_against_oracle(shape):
     from muon_fusion_ascend950_amd import capi
 
