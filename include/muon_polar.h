@@ -15,10 +15,10 @@
  * (the step of the transposed input, transposed back, without the copies; it
  * needs n % 8 == 0 and 16-byte aligned x and y, and A below is then G).  A and
  * P live in a caller-provided scratch ("workspace") of shape [batch,
- * padded_rows, padded_rows] each, where padded_rows >= min(m, n) is the stage
- * tile multiple reported by muon_polar_query().  The padding rows and columns
- * of A and P are written as exact zeros by the kernels, so no caller memset is
- * needed.
+ * padded_rows, padded_rows] each, where padded_rows >= min(m, n) is the larger
+ * of the gram and poly stages' tile extents, reported by muon_polar_query().  The
+ * padding rows and columns of A and P are written as exact zeros by the kernels,
+ * so no caller memset is needed.
  *
  * Stream-K: when the last round of a stage's output tiles would leave most CUs
  * idle, the K loops of those tiles are cut into equal shares, one per

@@ -165,6 +165,17 @@ uint32_t default_sym_tile(int64_t batch, int64_t s, int64_t large_from, int cus)
     if (batch * (t * (t + 1) / 2) * 2 >= cus) return 128;
     return 64;
 }
+// Poly's tile where 256x256 tiles would leave most CUs idle (a partial round cut
+// by stream-K) and 192x192 tiles fill one round to over 3/4: [4096,14336] poly
+// 91 -> 80 us per step (136 tiles of 256 against 253 of 192 on 256 CUs, no
+// split, no fix-ups).  Gram keeps its 256x256 split there: with 224 K-steps per
+// tile the split's fixed costs weigh less than 192x192 tiles' lower MFMA rate
+// (224 against 244 us); [4,4096,4096] keeps 256x256 (297 against 325 us).
+bool one_round_of_192(int64_t batch, int64_t s, int cus) {
+    const int64_t t192 = ceil_div(s, 192), t256 = ceil_div(s, 256);
+    const int64_t tiles = batch * (t192 * (t192 + 1) / 2);
+    return cus > 0 && batch * (t256 * (t256 + 1) / 2) < cus && tiles <= cus && 4 * tiles > 3 * cus;
+}
 uint32_t default_apply_tile(int64_t batch, int64_t m, int64_t n, int cus) {
     for (int64_t t : {256, 128})
         if (batch * ceil_div(m, t) * ceil_div(n, t) >= cus) return static_cast<uint32_t>(t);
@@ -201,9 +212,10 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
         env_u64("MUON_POLAR_GRAM_TILE", default_sym_tile(batch, s, 3072, cus)));
     // an explicit gram tile also sets the poly tile unless that is given too
     const bool gram_set = std::getenv("MUON_POLAR_GRAM_TILE") != nullptr;
+    uint32_t poly_tile = default_sym_tile(batch, s, 4096, cus);
+    if (poly_tile == 256 && one_round_of_192(batch, s, cus)) poly_tile = 192;
     k.poly_tile = static_cast<uint32_t>(
-        env_u64("MUON_POLAR_POLY_TILE",
-                gram_set ? k.gram_tile : default_sym_tile(batch, s, 4096, cus)));
+        env_u64("MUON_POLAR_POLY_TILE", gram_set ? k.gram_tile : poly_tile));
     k.apply_bm = static_cast<uint32_t>(
         env_u64("MUON_POLAR_APPLY_TILE_M", default_apply_tile(batch, m, n, cus)));
     k.apply_bn = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_TILE_N", k.apply_bm));
@@ -313,12 +325,13 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
     p.s = small;
     p.tall = tall;
     (void)large;
-    // A and P are tiled by both stage tiles: pad to a common multiple.
-    p.mp = round_up(small, std::lcm(p.gram_tile, p.poly_tile));
+    // A and P are [mp, mp] with mp the larger of the two stages' tile extents.
+    const int64_t ext_gram = round_up(small, p.gram_tile), ext_poly = round_up(small, p.poly_tile);
+    p.mp = std::max(ext_gram, ext_poly);
     if (p.mp * p.mp >= kMaxMatrixElems)
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "matrix too large (2^30 elements or more)");
-    p.gram_nt = static_cast<int>(p.mp / p.gram_tile);
-    p.poly_nt = static_cast<int>(p.mp / p.poly_tile);
+    p.gram_nt = static_cast<int>(ext_gram / p.gram_tile);
+    p.poly_nt = static_cast<int>(ext_poly / p.poly_tile);
     p.apply_tm = static_cast<int>((m + p.apply_bm - 1) / p.apply_bm);
     p.apply_tn = static_cast<int>((n + p.apply_bn - 1) / p.apply_bn);
     p.gram_grid = batch * (int64_t(p.gram_nt) * (p.gram_nt + 1) / 2);
@@ -891,6 +904,14 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
             lo = base + std::min(int64_t(row0) * g.ld_out + col0, int64_t(col0) * g.ld_out + row0);
             hi = base + std::max(int64_t(row0 + L.bm - 1) * g.ld_out + col0 + L.bn,
                                  int64_t(col0 + L.bn - 1) * g.ld_out + row0 + L.bm);
+            // last column tile: the zeros past the tile grid (zero_past_grid)
+            const int ext = g.tiles_n * L.bn;
+            if (col0 + L.bn == ext && g.ld_out > ext) {
+                const int w = g.ld_out - ext;
+                const int cols = row0 + L.bm == ext ? L.bm + w : L.bm;
+                hi = std::max({hi, base + int64_t(row0 + L.bm - 1) * g.ld_out + g.ld_out,
+                               base + int64_t(g.ld_out - 1) * g.ld_out + row0 + cols});
+            }
         } else {
             const int last_row = std::min(row0 + L.bm, g.out_rows) - 1;
             if (last_row < row0 || col0 >= g.out_cols) return;

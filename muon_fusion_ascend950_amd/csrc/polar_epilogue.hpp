@@ -48,6 +48,32 @@ __device__ __forceinline__ void epilogue_values(const f32x16 &acc, int q, const 
     }
 }
 
+// Symmetric stages write A or P as [mp, mp] (row stride ld_out = mp) from a grid
+// of tiles_n x tiles_n tiles of T rows; mp is the larger of the two symmetric
+// stages' tile extents, so a stage with the smaller tile stops short of it.  The
+// last column tile of each tile row then also writes zeros into its T rows past
+// the grid and into the mirrored rows (the last tile row covers the corner), so
+// the padding holds exact zeros whichever stage has the larger tile.
+template <int T>
+__device__ __forceinline__ void zero_past_grid(const GemmArgs &g, uint16_t *out, int tm, int tn,
+                                               int tid, int nthreads) {
+    const int ext = g.tiles_n * T;
+    const int w = g.ld_out - ext;  // a multiple of 64
+    if (w <= 0 || tn != g.tiles_n - 1) return;
+    const int row0 = tm * T;
+    const u32x4 z{0u, 0u, 0u, 0u};
+    const int wch = w >> 3;  // 16-byte chunks per row of the strip
+    for (int idx = tid; idx < T * wch; idx += nthreads) {
+        const int r = idx / wch, c = idx - r * wch;
+        *reinterpret_cast<u32x4 *>(out + (row0 + r) * g.ld_out + ext + 8 * c) = z;
+    }
+    const int cch = (tm == g.tiles_m - 1 ? T + w : T) >> 3;
+    for (int idx = tid; idx < w * cch; idx += nthreads) {
+        const int r = idx / cch, c = idx - r * cch;
+        *reinterpret_cast<u32x4 *>(out + (ext + r) * g.ld_out + row0 + 8 * c) = z;
+    }
+}
+
 template <int BM, int BN, Stage S, bool VEC>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[BM / 64][BN / 64], const GemmArgs &g,
                                            int bt, int row0, int col0, bool diag_tile, int lane,

@@ -15,9 +15,10 @@
 // (BM/2) x (BN/2) sub-tile of 32x32 MFMA blocks.  The K loop stages 64-deep
 // panels of both operands through LDS with a register prefetch of the next panel.
 //
-// Scratch layout: A and P are [batch][mp][mp] bf16 with mp a multiple of the
-// stage-1/2 tile; rows/columns >= m are computed from zero-filled X rows and are
-// therefore exact zeros, so stages 2 and 3 need no K masking on A or P.
+// Scratch layout: A and P are [batch][mp][mp] bf16 with mp the larger of the
+// stage-1/2 tile extents; rows/columns >= m are computed from zero-filled X rows
+// (or written as zeros past a stage's tile grid) and are therefore exact zeros, so
+// stages 2 and 3 need no K masking on A or P.
 #include "polar_kernels.h"
 #include "polar_schedule.hpp"
 #include "polar_tile.hpp"
@@ -118,6 +119,7 @@ __global__ __launch_bounds__(256) void polar_gemm_kernel(GemmArgs g) {
 
     // ---------------------------------------------------------------- epilogue
     store_tile<BM, BN, S, VEC>(acc, g, bt, row0, col0, tm == tn, lane, wr, wc);
+    if constexpr (S != Stage::Apply) zero_past_grid<BM>(g, g.out + bt * g.sb_out, tm, tn, tid, NT);
 }
 
 template <int BM, int BN, Stage S, bool VEC>

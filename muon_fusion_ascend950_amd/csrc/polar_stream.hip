@@ -749,6 +749,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
                 *reinterpret_cast<u32x4 *>(out + (col0 + mc) * g.ld_out + row0 + 8 * rb) = v;
             }
         }
+        zero_past_grid<BM>(g, out, tm, tn, tid, kThreads);
     }
 }
 
@@ -792,7 +793,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
 // per SIMD, 64x32 wave tiles; [16,512,2048] 62.5 -> 59.0 us, [1,1024,4096]
 // 46.3 -> 43.9 us against 4 waves); other tiles with 4 waves and the depths their
 // LDS allows (64x64: 2, 4 or 8 of 16 KiB; 128x256 and 256x128: 2 or 3 of 48 KiB;
-// 192x192: 2).
+// 192x192: 2; a third 48 KiB slot measured no faster at [4096,14336]).
 template <int BM, int BN>
 constexpr bool depth_ok(int waves, int depth) {
     if (BM == 256 && BN == 256) return depth == 2 && (waves == 8 || waves == 4);

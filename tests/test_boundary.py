@@ -343,11 +343,11 @@ def test_tuning_variables_enter_the_plan(monkeypatch):
     monkeypatch.setenv("MUON_POLAR_GRAM_TILE", "64")
     monkeypatch.setenv("MUON_POLAR_POLY_TILE", "64")
     assert capi.query(1, 300, 700).padded_rows == 320
-    # A and P are padded to a common multiple of the two stage tiles
+    # A and P are padded to the larger of the two stages' tile extents
     monkeypatch.setenv("MUON_POLAR_GRAM_TILE", "192")
     assert capi.query(1, 300, 700).padded_rows == 384
     monkeypatch.setenv("MUON_POLAR_POLY_TILE", "256")
-    assert capi.query(1, 300, 700).padded_rows == 768
+    assert capi.query(1, 300, 700).padded_rows == 512
 
 
 def test_build_entry_does_not_import_the_package():

@@ -61,17 +61,39 @@ def test_other_plans_store_inside_their_buffers(shape, occ):
     check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
 
 
-def test_headline_plan_splits_every_stage():
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)])
+def test_headline_plan(shape):
     """The walk covers the stream-K path: at [4096,14336] with one 256x256
-    workgroup per CU every stage cuts its last round."""
-    plan = capi.check_plan(1, 4096, 14336, cus=256, blocks_per_cu=(1, 1, 1))
-    for s in range(3):
+    workgroup per CU gram and apply cut their last round; poly runs one round
+    of 192x192 tiles (253 on 256 CUs), so A and P are padded to 4224 rows and
+    gram writes zeros past its 4096-row tile grid."""
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(1, 1, 1))
+    check(plan)
+    for s in (0, 2):
         e = plan.stage[s]
         assert (e.tile_m, e.tile_n, e.waves) == (256, 256, 8)
         assert e.sk_units > 0 and e.dp_tiles < e.total_tiles
     # gram: 136 upper tiles, all in the split; apply: 896 tiles, 3 whole rounds
     assert plan.stage[0].total_tiles == 136 and plan.stage[0].dp_tiles == 0
     assert plan.stage[2].total_tiles == 896 and plan.stage[2].dp_tiles == 768
+    poly = plan.stage[1]
+    assert (poly.tile_m, poly.tile_n, poly.total_tiles, poly.sk_units) == (192, 192, 253, 0)
+    # gram's zeros past its grid reach the last byte of A
+    assert plan.stage[0].out_hi == plan.stage[0].out_limit == 4224 * 4224 * 2
+
+
+@pytest.mark.parametrize("gram,poly", [(256, 192), (192, 256), (64, 192), (192, 128), (128, 64)])
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (2, 300, 1000), (3, 136, 200), (1, 1000, 3000)])
+def test_unequal_symmetric_tiles_store_inside_their_buffers(monkeypatch, gram, poly, shape):
+    """A and P are padded to the larger of the two stages' tile extents; the stage
+    with the smaller one also writes zeros up to it, inside the buffer."""
+    monkeypatch.setenv("MUON_POLAR_GRAM_TILE", str(gram))
+    monkeypatch.setenv("MUON_POLAR_POLY_TILE", str(poly))
+    s = min(shape[1:])
+    mp = max(-(-s // gram) * gram, -(-s // poly) * poly)
+    assert capi.query(*shape).padded_rows == mp
+    for occ in [(1, 1, 1), (2, 2, 2)]:
+        check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
 
 
 @pytest.mark.parametrize("env", [{"MUON_POLAR_WAVES": "4"},

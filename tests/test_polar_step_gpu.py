@@ -444,6 +444,46 @@ def test_tile_configuration_does_not_change_results(monkeypatch, stream, env):
     assert torch.equal(base, other)
 
 
+@pytest.mark.parametrize("tiles", [(256, 192), (192, 256), (64, 192), (128, 64)])
+@pytest.mark.parametrize("stream", ["1", "0"])
+@pytest.mark.parametrize("shape", [(2, 300, 1000), (1, 136, 200)])
+def test_unequal_symmetric_tiles_pad_with_zeros(monkeypatch, tiles, stream, shape):
+    """A and P are [mp, mp] with mp the larger of the gram and poly tile extents; the
+    stage with the smaller tile writes zeros past its tile grid.  Buffers filled with
+    NaN bits first: the padding must come back as exact zeros, and A, P and Y equal
+    those of equal tiles bit for bit (unsplit, both kernel families)."""
+    from muon_fusion_ascend950_amd import capi
+
+    a, b, c = C0
+    batch, m, n = shape
+    monkeypatch.setenv("MUON_POLAR_STREAM", stream)
+    monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
+    x = O.make_input(shape, seed=26).to(DEV)
+
+    def stages():
+        mp = capi.query(batch, m, n).padded_rows
+        gram = torch.full((batch, mp, mp), float("nan"), dtype=torch.bfloat16, device=DEV)
+        poly = torch.full_like(gram, float("nan"))
+        y = torch.full_like(x, float("nan"))
+        capi.gram(x, gram)
+        capi.poly(gram, poly, batch, m, n, b, c)
+        capi.apply(poly, x, y, a)
+        torch.cuda.synchronize()
+        return gram, poly, y, mp
+
+    g0, p0, y0, _ = stages()
+    monkeypatch.setenv("MUON_POLAR_GRAM_TILE", str(tiles[0]))
+    monkeypatch.setenv("MUON_POLAR_POLY_TILE", str(tiles[1]))
+    g1, p1, y1, mp = stages()
+    ext = [-(-m // t) * t for t in tiles]
+    print(f"tiles {tiles} stream {stream} shape {shape}: mp {mp}, extents {ext}", flush=True)
+    assert mp == max(ext)
+    for t1, t0 in ((g1, g0), (p1, p0)):
+        assert torch.equal(t1[:, :m, :m], t0[:, :m, :m])
+        assert bits(t1[:, m:, :]).max(initial=0) == 0 and bits(t1[:, :, m:]).max(initial=0) == 0
+    assert torch.equal(y1, y0)
+
+
 @pytest.mark.parametrize("env", [
     {"MUON_POLAR_GRAM_TILE": "64", "MUON_POLAR_POLY_TILE": "64", "MUON_POLAR_APPLY_TILE_M": "64",
      "MUON_POLAR_GRAM_DEPTH": "4", "MUON_POLAR_POLY_DEPTH": "8", "MUON_POLAR_APPLY_DEPTH": "2"},
