@@ -62,11 +62,12 @@ struct Knobs {
                         // bit 0 gram, bit 1 poly, bit 2 apply (0: off everywhere)
     uint32_t waves;     // waves per workgroup of the 256x256 DMA-fed kernels (4 or 8)
     uint32_t depth[3];  // LDS ring slots of each stage's DMA-fed kernel (0: by shape)
+    uint32_t pair;      // 1: 192x192 tiles run the 8-wave wave-pair kernels when waves == 8
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
                apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k &&
                waves == o.waves && depth[0] == o.depth[0] && depth[1] == o.depth[1] &&
-               depth[2] == o.depth[2];
+               depth[2] == o.depth[2] && pair == o.pair;
     }
 };
 
@@ -97,6 +98,7 @@ struct PlanKeyHash {
         mix(k.knobs.stream_k);
         mix(k.knobs.waves);
         mix(uint64_t(k.knobs.depth[0]) << 16 | uint64_t(k.knobs.depth[1]) << 8 | k.knobs.depth[2]);
+        mix(k.knobs.pair);
         return static_cast<size_t>(h);
     }
 };
@@ -165,12 +167,11 @@ uint32_t default_sym_tile(int64_t batch, int64_t s, int64_t large_from, int cus)
     if (batch * (t * (t + 1) / 2) * 2 >= cus) return 128;
     return 64;
 }
-// Poly's tile where 256x256 tiles would leave most CUs idle (a partial round cut
-// by stream-K) and 192x192 tiles fill one round to over 3/4: [4096,14336] poly
-// 91 -> 80 us per step (136 tiles of 256 against 253 of 192 on 256 CUs, no
-// split, no fix-ups).  Gram keeps its 256x256 split there: with 224 K-steps per
-// tile the split's fixed costs weigh less than 192x192 tiles' lower MFMA rate
-// (224 against 244 us); [4,4096,4096] keeps 256x256 (297 against 325 us).
+// The symmetric stages' tile where 256x256 tiles would leave most CUs idle (a
+// partial round cut by stream-K) and 192x192 tiles fill one round to over 3/4:
+// [4096,14336] poly 91 -> 80 us per step (136 tiles of 256 against 253 of 192 on
+// 256 CUs, no split, no fix-ups); gram with the wave-pair kernels (read_knobs).
+// [4,4096,4096] keeps 256x256 (poly 297 against 325 us).
 bool one_round_of_192(int64_t batch, int64_t s, int cus) {
     const int64_t t192 = ceil_div(s, 192), t256 = ceil_div(s, 256);
     const int64_t tiles = batch * (t192 * (t192 + 1) / 2);
@@ -208,8 +209,20 @@ int default_depth(int bm, int bn, int64_t tiles, int cus) {
 // X is [batch, m, n]; s = min(m, n) is the extent of A and P.
 int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     const int64_t s = std::min(m, n);
-    k.gram_tile = static_cast<uint32_t>(
-        env_u64("MUON_POLAR_GRAM_TILE", default_sym_tile(batch, s, 3072, cus)));
+    k.waves = static_cast<uint32_t>(env_u64("MUON_POLAR_WAVES", kDefaultWaves));
+    if (k.waves != 4 && k.waves != 8)
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_WAVES must be 4 or 8");
+    k.pair = static_cast<uint32_t>(env_u64("MUON_POLAR_PAIR", 1));
+    if (k.pair > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_PAIR must be 0 or 1");
+    // Gram takes 192x192 tiles where poly does (one round of them fills the CUs,
+    // below) when they run the wave-pair kernels and X rows are its K (m <= n):
+    // [4096,14336] gram 234.4 -> 226.9 us (253 unsplit tiles against 136 tiles
+    // of 256x256 cut by stream-K; 4-wave 192x192 tiles: 237.1 us).
+    uint32_t gram_tile = default_sym_tile(batch, s, 3072, cus);
+    if (gram_tile == 256 && m <= n && k.waves == 8 && k.pair == 1 &&
+        one_round_of_192(batch, s, cus))
+        gram_tile = 192;
+    k.gram_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_TILE", gram_tile));
     // an explicit gram tile also sets the poly tile unless that is given too
     const bool gram_set = std::getenv("MUON_POLAR_GRAM_TILE") != nullptr;
     uint32_t poly_tile = default_sym_tile(batch, s, 4096, cus);
@@ -228,9 +241,6 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     const uint64_t sk_stages = env_u64("MUON_POLAR_STREAM_K_STAGES", 7);
     if (sk_stages > 7) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_STREAM_K_STAGES must be 0..7");
     k.stream_k *= static_cast<uint32_t>(sk_stages);
-    k.waves = static_cast<uint32_t>(env_u64("MUON_POLAR_WAVES", kDefaultWaves));
-    if (k.waves != 4 && k.waves != 8)
-        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_WAVES must be 4 or 8");
     k.depth[0] = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_DEPTH", 0));
     k.depth[1] = static_cast<uint32_t>(env_u64("MUON_POLAR_POLY_DEPTH", 0));
     k.depth[2] = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_DEPTH", 0));
@@ -365,7 +375,10 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
     p.counter_stride = 0;
     size_t partial_bytes = 0;
     for (int s = 0; s < 3; ++s) {
-        p.waves[s] = muon_polar::stream_waves(tiles_bm[s], tiles_bn[s], static_cast<int>(knobs.waves));
+        // 192x192 tiles: 8 waves are the wave-pair kernels (MUON_POLAR_PAIR=0: 4 waves)
+        const bool no_pair = tiles_bm[s] == 192 && knobs.pair == 0;
+        p.waves[s] = muon_polar::stream_waves(tiles_bm[s], tiles_bn[s],
+                                              no_pair ? 4 : static_cast<int>(knobs.waves));
         p.depth[s] = knobs.depth[s] != 0
                          ? static_cast<int>(knobs.depth[s])
                          : default_depth(tiles_bm[s], tiles_bn[s], grids[s], cus);

@@ -32,6 +32,8 @@
 #include "polar_schedule.hpp"
 #include "polar_tile.hpp"
 
+#include <type_traits>
+
 namespace muon_polar {
 
 namespace {
@@ -111,10 +113,24 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
                                                int lt, int kbeg, int kend) {
     using Geo = StreamGeom<BM, BN, NW, D>;
     constexpr int kThreads = Geo::kThreads;
-    constexpr int WM = BM / 2, WN = BN / (NW / 2);
+    // Wave pairs (8 waves on a 192x192 tile, whose 2 x 4 wave grid would not be
+    // made of 32-wide MFMA blocks): the tile is four 96x96 wave tiles, each
+    // computed by two waves — wave w and w + 4 — that split every K-step's four
+    // k16 slices between them (slices h and h + 2 for h = w / 4).  Each wave pair
+    // reads each fragment once, as one wave of the 4-wave kernel does, and the two
+    // waves cover each other's LDS and barrier waits.  The halves are added once
+    // after the K loop (acc(h = 0) + acc(h = 1)), so each output sums its K terms
+    // in two interleaved chains: results differ in rounding from the 4-wave kernel.
+    constexpr bool kPair = NW == 8 && BM == 192;
+    constexpr int kGridWaves = kPair ? 4 : NW;
+    constexpr int WM = BM / 2, WN = BN / (kGridWaves / 2);
     constexpr int SM = WM / 32, SN = WN / 32;
     constexpr int kMfmaPerSlice = SM * SN;
+    // Threads that hold accumulators (the h = 0 waves in pair mode).
+    constexpr int kAccThreads = kPair ? kThreads / 2 : kThreads;
     using Tr = StageTraits<S>;
+    static_assert(!kPair || (BM == BN && Tr::kSymmetric && !Tr::kRowNC && !Tr::kColNC),
+                  "wave pairs serve the K-contiguous symmetric stages");
     static_assert(!Tr::kSymmetric || BM == BN, "triangular stages need square tiles");
     static_assert(!Tr::kRowNC || 512 % BM == 0, "N-contiguous panel rows must tile 1 KiB");
     static_assert(!Tr::kColNC || 512 % BN == 0, "N-contiguous panel rows must tile 1 KiB");
@@ -137,7 +153,10 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     constexpr bool kStepFrags = kMfmaPerSlice == 1;
     uint32_t &s_arrived = *s_arrived_p;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-    const int wr = wave & 1, wc = wave >> 1;
+    const int wq = kPair ? (wave & 3) : wave;  // wave tile of this wave
+    const int wr = wq & 1, wc = wq >> 1;
+    const int kh = kPair ? (wave >> 2) : 0;    // pair mode: which half of the slices
+    const bool acc_owner = !kPair || kh == 0;  // holds the tile's sums after the K loop
     const int nk = g.k_steps;
     const uint32_t smem_base = lds_addr(smem);
     const int64_t tstart = int64_t(lt) * nk;
@@ -384,13 +403,13 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // faster at 4096 x 14336 than reading them all first).
     auto mfmas_with_dma_frags = [&](const bf16x8 (&fr)[SM], const bf16x8 (&fc)[SN], int step,
                                     int slot_, bool live, int nslot,
-                                    bf16x8 (&nfr)[SM], bf16x8 (&nfc)[SN]) {
+                                    bf16x8 (&nfr)[SM], bf16x8 (&nfc)[SN], int nkk) {
 #pragma unroll
         for (int m = 0; m < kMfmaPerSlice; ++m) {
             const int i = m / SN, j = m % SN;
             acc[i][j] = mfma_32x32x16(fc[j], fr[i], acc[i][j]);
             __builtin_amdgcn_sched_barrier(0);
-            if (m < SM + SN) load_frag(nslot, 0, m, nfr, nfc);
+            if (m < SM + SN) load_frag(nslot, nkk, m, nfr, nfc);
 #pragma unroll
             for (int d = m * Geo::kLoads / kMfmaPerSlice;
                  d < (m + 1) * Geo::kLoads / kMfmaPerSlice; ++d)
@@ -398,7 +417,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int f = kMfmaPerSlice; f < SM + SN; ++f) load_frag(nslot, 0, f, nfr, nfc);
+        for (int f = kMfmaPerSlice; f < SM + SN; ++f) load_frag(nslot, nkk, f, nfr, nfc);
     };
     static_assert(kBK / 16 == 4, "schedule below is written for four k16 slices per step");
 
@@ -430,7 +449,38 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
         wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
     }
     int slot = 0;
-    if constexpr (kStepFrags) {
+    if constexpr (kPair) {
+        // This wave's k16 slices of every K-step: ka = h and kb = h + 2, in the
+        // 4-wave kernel's schedule with two slices per step:
+        //   frags(kb) | mfma(ka) | wait panel k+1, barrier | frags(next ka) |
+        //   mfma(kb) + DMA panel k+kStages -> slot
+        const int ka = kh, kb = kh + 2;
+        bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
+        load_frags(0, ka, fr0, fc0);
+        for (int k = 0; k < nkl; ++k) {
+            const int next = slot + 1 == kStages ? 0 : slot + 1;
+            load_frags(slot, kb, fr1, fc1);
+            mfmas(fr0, fc0);
+            for (int z = 0; z < kMfmaPerSlice; ++z) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // the waits of the schedule below (panel k+1; later DMA groups in flight)
+            const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+            if (kEpiPrefetch && k > nkl - kStages)
+                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
+            else
+                wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
+            mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
+                                 fc0, ka);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kEpiPrefetch) {
+                if (k == nkl - kStages) issue_epi(epi_slot);
+            }
+            slot = next;
+        }
+    } else if constexpr (kStepFrags) {
         // One MFMA per k16 slice (32x32 wave tiles): a slice's fragment reads
         // cannot hide behind the single MFMA issued before them, so every slice
         // would wait out the LDS latency.  Instead all fragments of step k+1 are
@@ -526,7 +576,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             else
                 wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
             mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
-                                 fc0);
+                                 fc0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (kEpiPrefetch) {
                 if (k == nkl - kStages) issue_epi(epi_slot);
@@ -536,6 +586,45 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     }
     // All waves are done with the ring (and no DMA is outstanding).
     wait_vm_barrier<0>();
+
+    // Wave pairs: the h = 1 wave's sums are added into its partner's through the
+    // ring, in two rounds of accumulator blocks (each round's buffer fits the
+    // ring): f32x4 group e4 of block f of wave tile wq at [wq][f][e4][lane].
+    if constexpr (kPair) {
+        constexpr int kF = SM * SN;
+        constexpr int kF0 = (kF + 1) / 2;
+        static_assert(4 * kF0 * 4 * 64 * 16 <= kStages * Geo::kStageBytes,
+                      "pair reduction buffer must fit the ring");
+        f32x4 *buf = reinterpret_cast<f32x4 *>(smem);
+        auto round = [&](auto lo_c, auto hi_c) {
+            constexpr int lo = decltype(lo_c)::value, hi = decltype(hi_c)::value;
+            if (kh == 1) {
+#pragma unroll
+                for (int f = lo; f < hi; ++f)
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4) {
+                        const f32x16 &a = acc[f / SN][f % SN];
+                        buf[((wq * kF0 + (f - lo)) * 4 + e4) * 64 + lane] =
+                            f32x4{a[4 * e4], a[4 * e4 + 1], a[4 * e4 + 2], a[4 * e4 + 3]};
+                    }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (kh == 0) {
+#pragma unroll
+                for (int f = lo; f < hi; ++f)
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4) {
+                        const f32x4 v = buf[((wq * kF0 + (f - lo)) * 4 + e4) * 64 + lane];
+                        f32x16 &a = acc[f / SN][f % SN];
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) a[4 * e4 + t] = a[4 * e4 + t] + v[t];
+                    }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        };
+        round(std::integral_constant<int, 0>{}, std::integral_constant<int, kF0>{});
+        round(std::integral_constant<int, kF0>{}, std::integral_constant<int, kF>{});
+    }
 
     // -------------------------------------------------------- stream-K fixup
     bool epi_issued = false;
@@ -564,10 +653,12 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
         auto lane_base = [&](int u) {
             return static_cast<uint32_t>(int64_t(sk_slot(u, lt)) * slot_bytes) + tid * 16;
         };
-        // Slot layout: 16-byte chunk c = (i * SN + j) * 4 + q of every thread,
-        // thread-minor, so each access instruction covers 1 KiB contiguously.
-        constexpr uint32_t kChunkStride = kThreads * 16;
+        // Slot layout: 16-byte chunk c = (i * SN + j) * 4 + q of every thread that
+        // holds accumulators, thread-minor, so each access instruction covers 1 KiB
+        // contiguously.
+        constexpr uint32_t kChunkStride = kAccThreads * 16;
         auto store_own = [&]() {
+            if (!acc_owner) return;
             const uint32_t base = lane_base(unit);
 #pragma unroll
             for (int i = 0; i < SM; ++i)
@@ -624,6 +715,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
         // Partials are read a row-block (16 chunks per lane) at a time, the
         // next block's loads in flight while the current one is added.
         auto add_partial = [&](int u, bool assign) {
+            if (!acc_owner) return;
             const uint32_t base = lane_base(u);
             // blocks of kBlk accumulator tiles (i, j), the next block's loads in
             // flight while one is added (one row-block of SN tiles; one tile
@@ -669,26 +761,29 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
         wait_vm_barrier<0>();
     }
 
-    // Each lane turns its accumulators into bf16 results in place.
+    // Each lane turns its accumulators into bf16 results in place (pair mode:
+    // the h = 0 waves, which hold the sums).
+    if (acc_owner) {
 #pragma unroll
-    for (int i = 0; i < SM; ++i) {
-        const int r = wr * WM + i * 32 + (lane & 31);
+        for (int i = 0; i < SM; ++i) {
+            const int r = wr * WM + i * 32 + (lane & 31);
 #pragma unroll
-        for (int j = 0; j < SN; ++j) {
+            for (int j = 0; j < SN; ++j) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
-                u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
-                float e[4] = {0.f, 0.f, 0.f, 0.f};
-                uint16_t h[4];
-                if constexpr (kAxInLoop) {
+                for (int q = 0; q < 4; ++q) {
+                    const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
+                    u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
+                    float e[4] = {0.f, 0.f, 0.f, 0.f};
+                    uint16_t h[4];
+                    if constexpr (kAxInLoop) {
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) h[t] = f32_to_bf16_bits(acc[i][j][4 * q + t]);
-                } else {
-                    if constexpr (kEpiLoad) unpack4(*p, e);
-                    epilogue_values<S>(acc[i][j], q, e, g, h);
+                        for (int t = 0; t < 4; ++t) h[t] = f32_to_bf16_bits(acc[i][j][4 * q + t]);
+                    } else {
+                        if constexpr (kEpiLoad) unpack4(*p, e);
+                        epilogue_values<S>(acc[i][j], q, e, g, h);
+                    }
+                    *p = pack4(h);
                 }
-                *p = pack4(h);
             }
         }
     }
@@ -798,6 +893,7 @@ template <int BM, int BN>
 constexpr bool depth_ok(int waves, int depth) {
     if (BM == 256 && BN == 256) return depth == 2 && (waves == 8 || waves == 4);
     if (BM == 128 && BN == 128) return (waves == 4 || waves == 8) && (depth == 2 || depth == 4);
+    if (BM == 192 && BN == 192) return depth == 2 && (waves == 8 || waves == 4);
     if (waves != 4) return false;
     if (BM == 64 && BN == 64) return depth == 2 || depth == 4 || depth == 8;
     if (BM != BN) return depth == 2 || depth == 3;
@@ -825,6 +921,9 @@ const void *kernel_for(int waves, int depth) {
                             : kernel_ptr<BM, BN, S, 4, 2, KT>();
     } else if constexpr (BM != BN) {
         return depth == 3 ? kernel_ptr<BM, BN, S, 4, 3, KT>() : kernel_ptr<BM, BN, S, 4, 2, KT>();
+    } else if constexpr (BM == 192) {
+        // 8 waves: wave pairs splitting the K-slices (symmetric stages only)
+        return waves == 8 ? kernel_ptr<BM, BN, S, 8, 2, KT>() : kernel_ptr<BM, BN, S, 4, 2, KT>();
     } else {
         return kernel_ptr<BM, BN, S, 4, 2, KT>();
     }
@@ -867,7 +966,7 @@ const void *stream_kernel(Stage s, int bm, int bn, int waves, int depth, bool kt
 }  // namespace
 
 int stream_waves(int bm, int bn, int requested) {
-    return (((bm == 256 && bn == 256) || (bm == 128 && bn == 128)) && requested == 8) ? 8 : 4;
+    return (bm == bn && (bm == 256 || bm == 192 || bm == 128) && requested == 8) ? 8 : 4;
 }
 
 bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth) {

@@ -68,6 +68,9 @@ def step_transposed(x, a, b, c):
 @pytest.mark.parametrize("shape", TALL_SHAPES)
 def test_unsplit_equals_transposed_path_bitwise(monkeypatch, shape):
     monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
+    # the transposed path's 192x192 wave-pair gram (two K chains per output) has no
+    # right-Gram counterpart: compare one-chain kernels on both routes
+    monkeypatch.setenv("MUON_POLAR_PAIR", "0")
     print(f"unsplit tall {shape}", flush=True)
     x = O.make_input(shape, seed=31).to(DEV)
     y = step_tall(x, *C0)
@@ -205,6 +208,7 @@ def test_express_tall(monkeypatch, shape, normalize):
     by an ulp), so with it the check is: normalise alone (no steps), then the steps
     without normalisation, gives the same bits."""
     monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
+    monkeypatch.setenv("MUON_POLAR_PAIR", "0")  # one K chain per output on both routes
     from muon_fusion_ascend950_amd import COEFFICIENTS, polar_express
 
     print(f"express tall {shape} normalize={normalize}", flush=True)
