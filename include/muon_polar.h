@@ -194,8 +194,12 @@ typedef struct muon_polar_stage_extent {
     int32_t tile_m, tile_n, waves, depth;
     int32_t dma_fed;       /* 1: DMA-fed kernel; 0: register-staged */
     int32_t k_steps, total_tiles, dp_tiles, sk_units, grid;
-    int32_t coverage_ok;   /* every (tile, K-step) iteration computed by exactly one workgroup */
+    int32_t coverage_ok;   /* every (tile, K-step) iteration computed by exactly one workgroup
+                              (a tile run as two column halves: once per half) */
     int32_t extents_ok;    /* per-matrix operand byte extents < 2^31 and passed unchanged */
+    int32_t halves;        /* 1: tiles past dp_tiles run as sk_units column halves, each over
+                              the whole K range (no partial slots, no arrival words) */
+    int32_t reserved;
     int64_t out_lo, out_hi, out_limit;          /* output stores, bytes: [lo, hi) vs buffer size */
     int64_t partial_lo, partial_hi, partial_limit; /* stream-K partial slots, bytes */
     int64_t counter_hi, counter_limit;          /* stream-K arrival words used vs reserved */

@@ -63,11 +63,12 @@ struct Knobs {
     uint32_t waves;     // waves per workgroup of the 256x256 DMA-fed kernels (4 or 8)
     uint32_t depth[3];  // LDS ring slots of each stage's DMA-fed kernel (0: by shape)
     uint32_t pair;      // 1: 192x192 tiles run the 8-wave wave-pair kernels when waves == 8
+    uint32_t halves;    // 1: apply's last round as 256x128 halves where it fits (below)
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
                apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k &&
                waves == o.waves && depth[0] == o.depth[0] && depth[1] == o.depth[1] &&
-               depth[2] == o.depth[2] && pair == o.pair;
+               depth[2] == o.depth[2] && pair == o.pair && halves == o.halves;
     }
 };
 
@@ -99,6 +100,7 @@ struct PlanKeyHash {
         mix(k.knobs.waves);
         mix(uint64_t(k.knobs.depth[0]) << 16 | uint64_t(k.knobs.depth[1]) << 8 | k.knobs.depth[2]);
         mix(k.knobs.pair);
+        mix(k.knobs.halves);
         return static_cast<size_t>(h);
     }
 };
@@ -107,8 +109,9 @@ struct PlanKeyHash {
 // workgroup, the rest cut into sk_units equal ranges of (tile, K-step) iterations.
 struct SkSplit {
     int64_t dp_tiles;
-    int32_t sk_units;
+    int32_t sk_units;  // stream-K units, or (halves) the number of 256x128 halves
     int64_t sk_iters;
+    bool halves;       // apply: the last round's tiles as 256x128 column halves
 };
 
 struct Plan {
@@ -214,6 +217,8 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_WAVES must be 4 or 8");
     k.pair = static_cast<uint32_t>(env_u64("MUON_POLAR_PAIR", 1));
     if (k.pair > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_PAIR must be 0 or 1");
+    k.halves = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_HALVES", 1));
+    if (k.halves > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_APPLY_HALVES must be 0 or 1");
     // Gram takes 192x192 tiles where poly does (one round of them fills the CUs,
     // below) when they run the wave-pair kernels and X rows are its K (m <= n):
     // [4096,14336] gram 234.4 -> 226.9 us (253 unsplit tiles against 136 tiles
@@ -291,7 +296,7 @@ int64_t sk_min_share(int bm, int bn) { return int64_t(bm) * bn >= 256 * 256 ? 20
 
 SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident, int64_t cus,
                   int64_t min_share) {
-    SkSplit c{tiles, 0, 0};
+    SkSplit c{tiles, 0, 0, false};
     if (!enabled || resident < 8) return c;
     const int64_t rem = tiles % resident;
     if (rem == 0 || rem * 4 > resident * 3 || rem * 4 > cus * 3) return c;
@@ -399,6 +404,22 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
                                                          p.waves[s], p.depth[s]);
         p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ, cus,
                             sk_min_share(tiles_bm[s], tiles_bn[s]));
+        // Apply's cut round as 256x128 column halves, one per workgroup, where the
+        // halves number between a half and a whole round of resident workgroups
+        // (each half is then as long as a stream-K share, or shorter): the same
+        // length of the last round without partials, arrival words or fix-ups.
+        // [4096,14336]: 128 tiles -> 256 halves.
+        if (s == 2 && p.sk[s].sk_units > 0 && knobs.halves == 1 && tiles_bm[s] == 256 &&
+            tiles_bn[s] == 256 && p.waves[s] == 8 && p.depth[s] == 2) {
+            const int64_t halves = 2 * (grids[s] - p.sk[s].dp_tiles);
+            const int64_t resident = int64_t(cus) * occ;
+            if (halves % 8 == 0 && 2 * halves > resident && halves <= resident) {
+                p.sk[s].sk_units = static_cast<int32_t>(halves);
+                p.sk[s].sk_iters = 0;
+                p.sk[s].halves = true;
+                continue;  // no partials, no arrival words
+            }
+        }
         if (p.sk[s].sk_units > 0) {
             p.sk_any = true;
             const int64_t sk_tiles = grids[s] - p.sk[s].dp_tiles;
@@ -749,14 +770,19 @@ void prepare_stage(StageLaunch &L, int64_t batch, const Plan &p, const SkArea *a
     g.dp_tiles = g.total_tiles;
     g.sk_units = 0;
     g.sk_iters = 0;
+    g.halves = 0;
     const SkSplit &sk = p.sk[L.sk_index];
     if (L.stream_ok && area != nullptr && sk.sk_units > 0) {
         g.dp_tiles = static_cast<int32_t>(sk.dp_tiles);
         g.sk_units = sk.sk_units;
         g.sk_iters = sk.sk_iters;
-        g.partials = area->partials;
-        g.counters = area->counters;
-        g.token = token;
+        if (sk.halves) {
+            g.halves = 1;  // whole tiles, then 256x128 halves: no partials or words
+        } else {
+            g.partials = area->partials;
+            g.counters = area->counters;
+            g.token = token;
+        }
     }
     g.per_xcd = (g.dp_tiles + 7) / 8;
 }
@@ -892,6 +918,8 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
     e.total_tiles = g.total_tiles;
     e.dp_tiles = g.dp_tiles;
     e.sk_units = g.sk_units;
+    e.halves = g.halves;
+    e.reserved = 0;
     e.grid = L.stream_ok ? g.sk_units + 8 * g.per_xcd : static_cast<int32_t>(L.grid);
     e.out_lo = INT64_MAX;
     e.out_hi = 0;
@@ -908,8 +936,9 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
     // (tile, K-step) iterations covered, to show each is computed exactly once
     std::vector<uint8_t> seen(static_cast<size_t>(g.total_tiles) * nk, 0);
     bool once = true;
-    auto store_tile = [&](int bt, int row0, int col0) {
-        // element range [lo, hi) of one workgroup's epilogue stores
+    auto store_tile = [&](int bt, int row0, int col0, int bn) {
+        // element range [lo, hi) of one workgroup's epilogue stores (a tile of
+        // L.bm x bn: bn = L.bn, or a 256x128 half of the apply stage's last round)
         int64_t lo, hi;
         if (sym) {
             // whole tile and its mirror, no bounds checks in the kernel
@@ -930,8 +959,8 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
             if (last_row < row0 || col0 >= g.out_cols) return;
             // last 16-byte chunk that starts inside the matrix; 8-element vector
             // stores when out_vec, else element stores up to the last column
-            const int last_chunk = col0 + 8 * ((std::min(col0 + L.bn, g.out_cols) - 1 - col0) / 8);
-            const int64_t end_col = g.out_vec ? last_chunk + 8 : std::min(col0 + L.bn, g.out_cols);
+            const int last_chunk = col0 + 8 * ((std::min(col0 + bn, g.out_cols) - 1 - col0) / 8);
+            const int64_t end_col = g.out_vec ? last_chunk + 8 : std::min(col0 + bn, g.out_cols);
             lo = int64_t(bt) * g.sb_out + int64_t(row0) * g.ld_out + col0;
             hi = int64_t(bt) * g.sb_out + int64_t(last_row) * g.ld_out + end_col;
         }
@@ -950,8 +979,43 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
                 tm = t % g.tiles_m;
                 tn = t / g.tiles_m;
             }
-            store_tile(bt, tm * L.bm, tn * L.bn);
+            store_tile(bt, tm * L.bm, tn * L.bn, L.bn);
             for (int k = 0; k < nk; ++k) once = once && seen[size_t(w) * nk + k]++ == 0;
+        }
+    } else if (g.halves) {
+        // polar_stream_halves_kernel: whole tiles, then two 256x128 halves per tile
+        // past dp_tiles, each over the whole K range (seen twice per K-step)
+        const int dp_grid = 8 * g.per_xcd;
+        for (int w = 0; w < e.grid; ++w) {
+            int tlin, half = -1;
+            if (w < dp_grid) {
+                tlin = (w & 7) * g.per_xcd + (w >> 3);
+                if (tlin >= g.dp_tiles) continue;
+            } else {
+                const int ws = w - dp_grid;
+                const int v = (ws & 7) * (g.sk_units >> 3) + (ws >> 3);
+                tlin = g.dp_tiles + (v >> 1);
+                half = v & 1;
+            }
+            if (tlin < 0 || tlin >= g.total_tiles) {
+                once = false;
+                continue;
+            }
+            const int bt = tlin / g.tiles_per_batch;
+            int tm, tn;
+            muon_polar::tile_coords(g, sym, tlin - bt * g.tiles_per_batch, tm, tn);
+            if (half < 0)
+                store_tile(bt, tm * L.bm, tn * L.bn, L.bn);
+            else
+                store_tile(bt, tm * L.bm, tn * L.bn + half * (L.bn / 2), L.bn / 2);
+            for (int k = 0; k < nk; ++k) ++seen[size_t(tlin) * nk + k];
+        }
+        // whole tiles once, halved tiles twice (one per half), nothing else
+        if (sym || L.bn != 256 || g.sk_units != 2 * (g.total_tiles - g.dp_tiles)) once = false;
+        for (size_t i = 0; i < seen.size(); ++i) {
+            const bool halved = int64_t(i / nk) >= g.dp_tiles;
+            once = once && seen[i] == (halved ? 2 : 1);
+            seen[i] = 1;
         }
     } else {
         for (int w = 0; w < e.grid; ++w) {
@@ -973,7 +1037,7 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
                 const int bt = tlin / g.tiles_per_batch;
                 int tm, tn;
                 muon_polar::tile_coords(g, sym, tlin - bt * g.tiles_per_batch, tm, tn);
-                store_tile(bt, tm * L.bm, tn * L.bn);
+                store_tile(bt, tm * L.bm, tn * L.bn, L.bn);
                 if (kbeg != 0 || kend != nk) {
                     // cut tile: arrival word lt, partial slots of its contributors
                     if (!splits || unit < 0) {

@@ -107,21 +107,26 @@ __device__ __forceinline__ int epi_offset(int row, int col) {
 // tile_base + lt (its stream-K fixup when the tile is cut, and its epilogue when
 // this workgroup completes it).  `smem`, `sink` and `s_arrived` are the caller's
 // LDS: the ring of D K-step slots, the per-wave DMA sink and one arrival word.
+// half >= 0: the segment computes column half `half` (BN wide) of the tile of
+// the launch's 2*BN-wide tile grid (the apply stage's last round, see
+// polar_stream_halves_kernel).
 template <int BM, int BN, Stage S, int NW, int D, bool KT>
 __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem, uint16_t *sink,
                                                uint32_t *s_arrived_p, int unit, int tile_base,
-                                               int lt, int kbeg, int kend) {
+                                               int lt, int kbeg, int kend, int half = -1) {
     using Geo = StreamGeom<BM, BN, NW, D>;
     constexpr int kThreads = Geo::kThreads;
     // Wave pairs (8 waves on a 192x192 tile, whose 2 x 4 wave grid would not be
-    // made of 32-wide MFMA blocks): the tile is four 96x96 wave tiles, each
-    // computed by two waves — wave w and w + 4 — that split every K-step's four
-    // k16 slices between them (slices h and h + 2 for h = w / 4).  Each wave pair
-    // reads each fragment once, as one wave of the 4-wave kernel does, and the two
-    // waves cover each other's LDS and barrier waits.  The halves are added once
-    // after the K loop (acc(h = 0) + acc(h = 1)), so each output sums its K terms
-    // in two interleaved chains: results differ in rounding from the 4-wave kernel.
-    constexpr bool kPair = NW == 8 && BM == 192;
+    // made of 32-wide MFMA blocks, or on a 256x128 apply tile, whose 2 x 4 grid
+    // would read 5 fragments per 4 MFMAs): the tile is four wave tiles (96x96,
+    // 128x64), each computed by two waves — wave w and w + 4 — that split every
+    // K-step's four k16 slices between them (slices h and h + 2 for h = w / 4).
+    // Each wave pair reads each fragment once, as one wave of a 4-wave kernel
+    // does, and the two waves cover each other's LDS and barrier waits.  The
+    // halves are added once after the K loop (acc(h = 0) + acc(h = 1)), so each
+    // output sums its K terms in two interleaved chains: results differ in
+    // rounding from the single-chain kernels.
+    constexpr bool kPair = NW == 8 && ((BM == 192 && BN == 192) || (BM == 256 && BN == 128));
     constexpr int kGridWaves = kPair ? 4 : NW;
     constexpr int WM = BM / 2, WN = BN / (kGridWaves / 2);
     constexpr int SM = WM / 32, SN = WN / 32;
@@ -129,8 +134,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // Threads that hold accumulators (the h = 0 waves in pair mode).
     constexpr int kAccThreads = kPair ? kThreads / 2 : kThreads;
     using Tr = StageTraits<S>;
-    static_assert(!kPair || (BM == BN && Tr::kSymmetric && !Tr::kRowNC && !Tr::kColNC),
-                  "wave pairs serve the K-contiguous symmetric stages");
+    static_assert(!kPair || !Tr::kRowNC, "wave pairs read a K-contiguous row operand");
     static_assert(!Tr::kSymmetric || BM == BN, "triangular stages need square tiles");
     static_assert(!Tr::kRowNC || 512 % BM == 0, "N-contiguous panel rows must tile 1 KiB");
     static_assert(!Tr::kColNC || 512 % BN == 0, "N-contiguous panel rows must tile 1 KiB");
@@ -172,7 +176,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     const int t = tlin - bt * g.tiles_per_batch;
     int tm, tn;
     tile_coords(g, Tr::kSymmetric, t, tm, tn);
-    const int row0 = tm * BM, col0 = tn * BN;
+    const int row0 = tm * BM, col0 = half >= 0 ? tn * (2 * BN) + half * BN : tn * BN;
 
     const i32x4 rs_row = make_buffer_rsrc(g.rowop + bt * g.sb_row, g.bytes_row);
     const i32x4 rs_col = make_buffer_rsrc(g.colop + bt * g.sb_col, g.bytes_col);
@@ -339,6 +343,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // per output element over the whole K loop.
     auto add_ax = [&](int slot, int kg) {
         if constexpr (kAxInLoop) {
+            if (!acc_owner) return;  // wave pairs: a·X goes into the h = 0 half once
             const uint16_t *as = smem + slot * (Geo::kStageBytes / 2);
             const uint16_t *bs = as + Geo::kABytes / 2;
             const float a = g.s_epi;
@@ -459,6 +464,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
         load_frags(0, ka, fr0, fc0);
         for (int k = 0; k < nkl; ++k) {
             const int next = slot + 1 == kStages ? 0 : slot + 1;
+            if constexpr (kAxInLoop) add_ax(slot, kbeg + k);
             load_frags(slot, kb, fr1, fc1);
             mfmas(fr0, fc0);
             for (int z = 0; z < kMfmaPerSlice; ++z) {
@@ -883,6 +889,36 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     }
 }
 
+// Apply stage whose last round of 256x256 tiles would leave most CUs idle:
+// whole 256x256 tiles [0, dp_tiles) one per workgroup (the first 8 * per_xcd
+// workgroups, XCD-contiguous runs as in polar_stream_kernel), then each tile of
+// [dp_tiles, total_tiles) as two 256x128 column halves, one per workgroup
+// (g.sk_units = the number of halves, a multiple of 8; XCD-contiguous runs of
+// halves).  A half computes its whole K range: no partials, no fix-up.  The
+// halves run the wave-pair kernel (two K chains per output).
+template <Stage S, bool KT>
+__global__ __launch_bounds__(512) void polar_stream_halves_kernel(GemmArgs g) {
+    using Geo = StreamGeom<256, 256, 8, 2>;
+    static_assert(StreamGeom<256, 128, 8, 2>::kStageBytes * 2 <= Geo::kStageBytes * 2,
+                  "the halves' ring fits the whole tiles' ring");
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * Geo::kStageBytes / 2];
+    __shared__ __attribute__((aligned(1024))) uint16_t sink[8 * 512];
+    __shared__ uint32_t s_arrived;
+    const int w = static_cast<int>(blockIdx.x);
+    const int dp_grid = 8 * g.per_xcd;
+    if (w < dp_grid) {
+        const int tile = (w & 7) * g.per_xcd + (w >> 3);
+        if (tile >= g.dp_tiles) return;
+        stream_segment<256, 256, S, 8, 2, KT>(g, smem, sink, &s_arrived, -1, tile, 0, 0,
+                                              g.k_steps);
+    } else {
+        const int ws = w - dp_grid;
+        const int v = (ws & 7) * (g.sk_units >> 3) + (ws >> 3);
+        stream_segment<256, 128, S, 8, 2, KT>(g, smem, sink, &s_arrived, -1, g.dp_tiles + (v >> 1),
+                                              0, 0, g.k_steps, v & 1);
+    }
+}
+
 // Instantiated (tile, waves, depth) combinations: 256x256 with 8 or 4 waves and
 // two slots; 128x128 with 8 or 4 waves and 2 or 4 slots of 32 KiB (8 waves: two
 // per SIMD, 64x32 wave tiles; [16,512,2048] 62.5 -> 59.0 us, [1,1024,4096]
@@ -973,8 +1009,35 @@ bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth) {
     return stream_kernel(s, bm, bn, waves, depth, false) != nullptr;
 }
 
+// The halves kernel of an apply stage (polar_stream_halves_kernel), or null.
+const void *halves_kernel(Stage s, bool kt) {
+    switch (s) {
+        case Stage::Apply:
+            return kt ? nullptr : reinterpret_cast<const void *>(
+                                      &polar_stream_halves_kernel<Stage::Apply, false>);
+        case Stage::ApplyR:
+            return kt ? reinterpret_cast<const void *>(
+                            &polar_stream_halves_kernel<Stage::ApplyR, true>)
+                      : reinterpret_cast<const void *>(
+                            &polar_stream_halves_kernel<Stage::ApplyR, false>);
+        default:
+            return nullptr;
+    }
+}
+
 hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const GemmArgs &g,
                          hipStream_t stream, bool k_mask) {
+    if (g.halves) {
+        // 256x256 whole tiles with 8 waves and two ring slots, then 256x128 halves
+        const void *k = bm == 256 && bn == 256 && waves == 8 && depth == 2
+                            ? halves_kernel(s, k_mask)
+                            : nullptr;
+        if (k == nullptr || g.sk_units % 8 != 0) return hipErrorInvalidValue;
+        const int grid = g.sk_units + 8 * g.per_xcd;
+        GemmArgs copy = g;
+        void *args[] = {&copy};
+        return hipLaunchKernel(k, dim3(grid), dim3(512), args, 0, stream);
+    }
     const void *k = stream_kernel(s, bm, bn, waves, depth, k_mask);
     if (k == nullptr) return hipErrorInvalidValue;
     const int grid = g.sk_units + 8 * g.per_xcd;

@@ -37,7 +37,12 @@ def check(plan: capi.PlanExtents) -> None:
         assert e.extents_ok == 1, f"stage {s}: an operand extent does not fit 32-bit offsets"
         assert 0 <= e.out_lo <= e.out_hi <= e.out_limit, (
             f"stage {s}: stores [{e.out_lo}, {e.out_hi}) outside an output of {e.out_limit} bytes")
-        if e.sk_units > 0:
+        if e.halves:
+            # apply's last round as column halves: whole K per half, nothing shared
+            assert s == 2 and e.dma_fed == 1 and (e.tile_m, e.tile_n, e.waves) == (256, 256, 8)
+            assert e.sk_units == 2 * (e.total_tiles - e.dp_tiles) > 0
+            assert e.partial_hi == 0 and e.counter_hi == 0
+        elif e.sk_units > 0:
             assert e.dma_fed == 1
             assert 0 <= e.partial_lo < e.partial_hi <= e.partial_limit, (
                 f"stage {s}: partial slots [{e.partial_lo}, {e.partial_hi}) outside "

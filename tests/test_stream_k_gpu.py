@@ -28,12 +28,16 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 C0 = O.COEFFICIENTS[0]
 EXACT_COEFFS = (2.0, -1.0, 1.0)
-# (batch, m, n): headline shape (all three stages split), batch crossing inside the
-# split range, ragged m and n (padded rows, partial last K-step, edge column tiles),
-# 128-row tiles.
-SPLIT_SHAPES = [(1, 4096, 14336), (2, 768, 8192), (1, 2000, 4040), (1, 1024, 8192)]
-# the same with 256x256 tiles for the triangular stages (256 KiB partials)
+# (batch, m, n): batch crossing inside the split range, ragged m and n (padded rows,
+# partial last K-step, edge column tiles), 64- and 128-row tiles.  (The headline
+# shape splits no stage by default: gram and poly run one round of 192x192 tiles and
+# apply's last round runs as 256x128 halves, test_halves_gpu.py; it is split here
+# with 256x256 triangular tiles, and with the halves off.)
+SPLIT_SHAPES = [(2, 768, 8192), (1, 2000, 4040), (1, 1024, 8192), (1, 2048, 8192)]
+# 256x256 tiles for the triangular stages (256 KiB partials)
 BIG_TILES = {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_POLY_TILE": "256"}
+# every stage of the headline split: 256x256 triangular tiles, apply's halves off
+HEADLINE_SPLIT = {**BIG_TILES, "MUON_POLAR_APPLY_HALVES": "0"}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -75,8 +79,8 @@ def test_split_is_in_use(shape):
 
 @pytest.mark.parametrize("split", ["1", "0"])
 @pytest.mark.parametrize("shape,env", [(s, {}) for s in SPLIT_SHAPES] +
-                         [((1, 4096, 14336), BIG_TILES), ((2, 2048, 4096), BIG_TILES),
-                          ((1, 4096, 14336), {**BIG_TILES, "MUON_POLAR_WAVES": "8"})])
+                         [((1, 4096, 14336), HEADLINE_SPLIT), ((2, 2048, 4096), BIG_TILES),
+                          ((1, 4096, 14336), BIG_TILES)])
 def test_exact_sums_are_bitwise(monkeypatch, shape, env, split):
     monkeypatch.setenv("MUON_POLAR_STREAM_K", split)
     for k, v in env.items():
