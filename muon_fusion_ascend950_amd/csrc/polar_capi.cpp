@@ -64,11 +64,13 @@ struct Knobs {
     uint32_t depth[3];  // LDS ring slots of each stage's DMA-fed kernel (0: by shape)
     uint32_t pair;      // 1: 192x192 tiles run the 8-wave wave-pair kernels when waves == 8
     uint32_t halves;    // 1: apply's last round as 256x128 halves where it fits (below)
+    uint32_t halves_depth;  // LDS ring slots of those halves (2 or 3)
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
                apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k &&
                waves == o.waves && depth[0] == o.depth[0] && depth[1] == o.depth[1] &&
-               depth[2] == o.depth[2] && pair == o.pair && halves == o.halves;
+               depth[2] == o.depth[2] && pair == o.pair && halves == o.halves &&
+               halves_depth == o.halves_depth;
     }
 };
 
@@ -101,6 +103,7 @@ struct PlanKeyHash {
         mix(uint64_t(k.knobs.depth[0]) << 16 | uint64_t(k.knobs.depth[1]) << 8 | k.knobs.depth[2]);
         mix(k.knobs.pair);
         mix(k.knobs.halves);
+        mix(k.knobs.halves_depth);
         return static_cast<size_t>(h);
     }
 };
@@ -111,7 +114,8 @@ struct SkSplit {
     int64_t dp_tiles;
     int32_t sk_units;  // stream-K units, or (halves) the number of 256x128 halves
     int64_t sk_iters;
-    bool halves;       // apply: the last round's tiles as 256x128 column halves
+    int32_t halves;    // apply: the last round's tiles as 256x128 column halves with
+                       // this many ring slots (0: not)
 };
 
 struct Plan {
@@ -203,9 +207,12 @@ int device_cus(int device) {
 // tiles (two workgroups per CU still fit) and 128x128 tiles when every tile has
 // a CU of its own anyway (poly at [2, 2048, 8192]: 288 -> 270 us per step).
 // Otherwise two: deeper rings lower the occupancy of the MFMA-bound shapes.
-int default_depth(int bm, int bn, int64_t tiles, int cus) {
+int default_depth(int bm, int bn, int waves, int64_t tiles, int cus) {
     if (bm == 64 && bn == 64) return 4;
     if (bm == 128 && bn == 128 && cus > 0 && tiles <= cus) return 4;
+    // 192x192 wave pairs: a third 48 KiB slot ([4096,14336] gram 225 -> 212 us,
+    // poly 75 -> 72 us; the LDS holds it, one workgroup per CU either way)
+    if (bm == 192 && bn == 192 && waves == 8) return 3;
     return 2;
 }
 
@@ -219,6 +226,10 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     if (k.pair > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_PAIR must be 0 or 1");
     k.halves = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_HALVES", 1));
     if (k.halves > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_APPLY_HALVES must be 0 or 1");
+    // three 48 KiB slots for the halves: [4096,14336] apply 395 -> 390 us
+    k.halves_depth = static_cast<uint32_t>(env_u64("MUON_POLAR_HALVES_DEPTH", 3));
+    if (k.halves_depth != 2 && k.halves_depth != 3)
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_HALVES_DEPTH must be 2 or 3");
     // Gram takes 192x192 tiles where poly does (one round of them fills the CUs,
     // below) when they run the wave-pair kernels and X rows are its K (m <= n):
     // [4096,14336] gram 234.4 -> 226.9 us (253 unsplit tiles against 136 tiles
@@ -296,7 +307,7 @@ int64_t sk_min_share(int bm, int bn) { return int64_t(bm) * bn >= 256 * 256 ? 20
 
 SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident, int64_t cus,
                   int64_t min_share) {
-    SkSplit c{tiles, 0, 0, false};
+    SkSplit c{tiles, 0, 0, 0};
     if (!enabled || resident < 8) return c;
     const int64_t rem = tiles % resident;
     if (rem == 0 || rem * 4 > resident * 3 || rem * 4 > cus * 3) return c;
@@ -386,12 +397,13 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
                                               no_pair ? 4 : static_cast<int>(knobs.waves));
         p.depth[s] = knobs.depth[s] != 0
                          ? static_cast<int>(knobs.depth[s])
-                         : default_depth(tiles_bm[s], tiles_bn[s], grids[s], cus);
+                         : default_depth(tiles_bm[s], tiles_bn[s], p.waves[s], grids[s], cus);
         if (p.stream && !muon_polar::stream_depth_supported(stages[s], tiles_bm[s], tiles_bn[s],
                                                             p.waves[s], p.depth[s]))
             return fail(MUON_POLAR_ERR_CONFIG,
                         "no DMA-fed kernel for this tile, wave count and MUON_POLAR_*_DEPTH "
-                        "(128x128: 2 or 4; 64x64: 2, 4 or 8; 128x256 / 256x128: 2 or 3; "
+                        "(128x128: 2 or 4; 64x64: 2, 4 or 8; 128x256 / 256x128: 2 or 3; 192x192: 2, or 3 "
+                        "with 8 waves; "
                         "others: 2)");
     }
     for (int s = 0; s < 3; ++s) {
@@ -416,7 +428,7 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
             if (halves % 8 == 0 && 2 * halves > resident && halves <= resident) {
                 p.sk[s].sk_units = static_cast<int32_t>(halves);
                 p.sk[s].sk_iters = 0;
-                p.sk[s].halves = true;
+                p.sk[s].halves = static_cast<int32_t>(knobs.halves_depth);
                 continue;  // no partials, no arrival words
             }
         }
@@ -777,7 +789,7 @@ void prepare_stage(StageLaunch &L, int64_t batch, const Plan &p, const SkArea *a
         g.sk_units = sk.sk_units;
         g.sk_iters = sk.sk_iters;
         if (sk.halves) {
-            g.halves = 1;  // whole tiles, then 256x128 halves: no partials or words
+            g.halves = sk.halves;  // whole tiles, then 256x128 halves: no partials or words
         } else {
             g.partials = area->partials;
             g.counters = area->counters;
@@ -918,7 +930,7 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
     e.total_tiles = g.total_tiles;
     e.dp_tiles = g.dp_tiles;
     e.sk_units = g.sk_units;
-    e.halves = g.halves;
+    e.halves = g.halves != 0 ? 1 : 0;
     e.reserved = 0;
     e.grid = L.stream_ok ? g.sk_units + 8 * g.per_xcd : static_cast<int32_t>(L.grid);
     e.out_lo = INT64_MAX;

@@ -71,10 +71,10 @@ struct GemmArgs {
     // launch (a captured graph keeps its token) reads as zero too.
     uint64_t *counters;
     uint32_t token;                 // this launch's token
-    // Apply stages (DMA-fed, 256x256 tiles with 8 waves): 1 = the tiles past
+    // Apply stages (DMA-fed, 256x256 tiles with 8 waves): 2 or 3 = the tiles past
     // dp_tiles run as two 256x128 column halves each, one per workgroup after the
-    // whole tiles, sk_units = the number of halves (no partials, no arrival
-    // words); 0 = the stream-K split above.
+    // whole tiles, with that many ring slots, sk_units = the number of halves (no
+    // partials, no arrival words); 0 = the stream-K split above.
     int32_t halves;
 };
 

@@ -896,12 +896,12 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
 // (g.sk_units = the number of halves, a multiple of 8; XCD-contiguous runs of
 // halves).  A half computes its whole K range: no partials, no fix-up.  The
 // halves run the wave-pair kernel (two K chains per output).
-template <Stage S, bool KT>
+template <Stage S, bool KT, int DH>
 __global__ __launch_bounds__(512) void polar_stream_halves_kernel(GemmArgs g) {
-    using Geo = StreamGeom<256, 256, 8, 2>;
-    static_assert(StreamGeom<256, 128, 8, 2>::kStageBytes * 2 <= Geo::kStageBytes * 2,
-                  "the halves' ring fits the whole tiles' ring");
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * Geo::kStageBytes / 2];
+    // ring: two 64 KiB slots for the whole tiles, DH 48 KiB slots for the halves
+    constexpr int kWhole = 2 * StreamGeom<256, 256, 8, 2>::kStageBytes;
+    constexpr int kHalf = DH * StreamGeom<256, 128, 8, DH>::kStageBytes;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[(kWhole > kHalf ? kWhole : kHalf) / 2];
     __shared__ __attribute__((aligned(1024))) uint16_t sink[8 * 512];
     __shared__ uint32_t s_arrived;
     const int w = static_cast<int>(blockIdx.x);
@@ -914,8 +914,8 @@ __global__ __launch_bounds__(512) void polar_stream_halves_kernel(GemmArgs g) {
     } else {
         const int ws = w - dp_grid;
         const int v = (ws & 7) * (g.sk_units >> 3) + (ws >> 3);
-        stream_segment<256, 128, S, 8, 2, KT>(g, smem, sink, &s_arrived, -1, g.dp_tiles + (v >> 1),
-                                              0, 0, g.k_steps, v & 1);
+        stream_segment<256, 128, S, 8, DH, KT>(g, smem, sink, &s_arrived, -1,
+                                               g.dp_tiles + (v >> 1), 0, 0, g.k_steps, v & 1);
     }
 }
 
@@ -929,7 +929,7 @@ template <int BM, int BN>
 constexpr bool depth_ok(int waves, int depth) {
     if (BM == 256 && BN == 256) return depth == 2 && (waves == 8 || waves == 4);
     if (BM == 128 && BN == 128) return (waves == 4 || waves == 8) && (depth == 2 || depth == 4);
-    if (BM == 192 && BN == 192) return depth == 2 && (waves == 8 || waves == 4);
+    if (BM == 192 && BN == 192) return (depth == 2 && waves == 4) || ((depth == 2 || depth == 3) && waves == 8);
     if (waves != 4) return false;
     if (BM == 64 && BN == 64) return depth == 2 || depth == 4 || depth == 8;
     if (BM != BN) return depth == 2 || depth == 3;
@@ -959,7 +959,9 @@ const void *kernel_for(int waves, int depth) {
         return depth == 3 ? kernel_ptr<BM, BN, S, 4, 3, KT>() : kernel_ptr<BM, BN, S, 4, 2, KT>();
     } else if constexpr (BM == 192) {
         // 8 waves: wave pairs splitting the K-slices (symmetric stages only)
-        return waves == 8 ? kernel_ptr<BM, BN, S, 8, 2, KT>() : kernel_ptr<BM, BN, S, 4, 2, KT>();
+        if (waves == 8)
+            return depth == 3 ? kernel_ptr<BM, BN, S, 8, 3, KT>() : kernel_ptr<BM, BN, S, 8, 2, KT>();
+        return kernel_ptr<BM, BN, S, 4, 2, KT>();
     } else {
         return kernel_ptr<BM, BN, S, 4, 2, KT>();
     }
@@ -1009,20 +1011,25 @@ bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth) {
     return stream_kernel(s, bm, bn, waves, depth, false) != nullptr;
 }
 
-// The halves kernel of an apply stage (polar_stream_halves_kernel), or null.
-const void *halves_kernel(Stage s, bool kt) {
+// The halves kernel of an apply stage (polar_stream_halves_kernel) with a ring of
+// `dh` slots for the halves (2 or 3), or null.
+template <int DH>
+const void *halves_kernel_d(Stage s, bool kt) {
     switch (s) {
         case Stage::Apply:
             return kt ? nullptr : reinterpret_cast<const void *>(
-                                      &polar_stream_halves_kernel<Stage::Apply, false>);
+                                      &polar_stream_halves_kernel<Stage::Apply, false, DH>);
         case Stage::ApplyR:
             return kt ? reinterpret_cast<const void *>(
-                            &polar_stream_halves_kernel<Stage::ApplyR, true>)
+                            &polar_stream_halves_kernel<Stage::ApplyR, true, DH>)
                       : reinterpret_cast<const void *>(
-                            &polar_stream_halves_kernel<Stage::ApplyR, false>);
+                            &polar_stream_halves_kernel<Stage::ApplyR, false, DH>);
         default:
             return nullptr;
     }
+}
+const void *halves_kernel(Stage s, bool kt, int dh) {
+    return dh == 3 ? halves_kernel_d<3>(s, kt) : dh == 2 ? halves_kernel_d<2>(s, kt) : nullptr;
 }
 
 hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const GemmArgs &g,
@@ -1030,7 +1037,7 @@ hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const Ge
     if (g.halves) {
         // 256x256 whole tiles with 8 waves and two ring slots, then 256x128 halves
         const void *k = bm == 256 && bn == 256 && waves == 8 && depth == 2
-                            ? halves_kernel(s, k_mask)
+                            ? halves_kernel(s, k_mask, g.halves)
                             : nullptr;
         if (k == nullptr || g.sk_units % 8 != 0) return hipErrorInvalidValue;
         const int grid = g.sk_units + 8 * g.per_xcd;
