@@ -225,18 +225,17 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     k.pair = static_cast<uint32_t>(env_u64("MUON_POLAR_PAIR", 1));
     if (k.pair > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_PAIR must be 0 or 1");
     k.halves = static_cast<uint32_t>(env_u64("MUON_POLAR_APPLY_HALVES", 1));
-    if (k.halves > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_APPLY_HALVES must be 0 or 1");
+    if (k.halves > 2) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_APPLY_HALVES must be 0, 1 or 2");
     // three 48 KiB slots for the halves: [4096,14336] apply 395 -> 390 us
     k.halves_depth = static_cast<uint32_t>(env_u64("MUON_POLAR_HALVES_DEPTH", 3));
     if (k.halves_depth != 2 && k.halves_depth != 3)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_HALVES_DEPTH must be 2 or 3");
     // Gram takes 192x192 tiles where poly does (one round of them fills the CUs,
-    // below) when they run the wave-pair kernels and X rows are its K (m <= n):
-    // [4096,14336] gram 234.4 -> 226.9 us (253 unsplit tiles against 136 tiles
-    // of 256x256 cut by stream-K; 4-wave 192x192 tiles: 237.1 us).
+    // below) when they run the wave-pair kernels: [4096,14336] gram 234.4 -> 226.9
+    // us (253 unsplit tiles against 136 tiles of 256x256 cut by stream-K; 4-wave
+    // 192x192 tiles: 237.1 us).  Both forms (X rows or X columns as its K).
     uint32_t gram_tile = default_sym_tile(batch, s, 3072, cus);
-    if (gram_tile == 256 && m <= n && k.waves == 8 && k.pair == 1 &&
-        one_round_of_192(batch, s, cus))
+    if (gram_tile == 256 && k.waves == 8 && k.pair == 1 && one_round_of_192(batch, s, cus))
         gram_tile = 192;
     k.gram_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_TILE", gram_tile));
     // an explicit gram tile also sets the poly tile unless that is given too
@@ -339,8 +338,6 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
                Plan &out) {
     const bool tall = m > n;
     const int64_t small = std::min(m, n), large = std::max(m, n);
-    if (tall && knobs.gram_tile == 192)
-        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_GRAM_TILE=192 is not available for m > n");
     Plan p{};
     p.gram_tile = static_cast<int>(knobs.gram_tile);
     p.poly_tile = static_cast<int>(knobs.poly_tile);
@@ -421,6 +418,13 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
         // (each half is then as long as a stream-K share, or shorter): the same
         // length of the last round without partials, arrival words or fix-ups.
         // [4096,14336]: 128 tiles -> 256 halves.
+        if (s == 2 && knobs.halves == 2 && sk_ok && tiles_bm[s] == 256 && tiles_bn[s] == 256 &&
+            p.waves[s] == 8 && p.depth[s] == 2 && (2 * grids[s]) % 8 == 0) {
+            // every tile as two halves
+            p.sk[s] = SkSplit{0, static_cast<int32_t>(2 * grids[s]), 0,
+                              static_cast<int32_t>(knobs.halves_depth)};
+            continue;
+        }
         if (s == 2 && p.sk[s].sk_units > 0 && knobs.halves == 1 && tiles_bm[s] == 256 &&
             tiles_bn[s] == 256 && p.waves[s] == 8 && p.depth[s] == 2) {
             const int64_t halves = 2 * (grids[s] - p.sk[s].dp_tiles);

@@ -134,10 +134,9 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // Threads that hold accumulators (the h = 0 waves in pair mode).
     constexpr int kAccThreads = kPair ? kThreads / 2 : kThreads;
     using Tr = StageTraits<S>;
-    static_assert(!kPair || !Tr::kRowNC, "wave pairs read a K-contiguous row operand");
     static_assert(!Tr::kSymmetric || BM == BN, "triangular stages need square tiles");
-    static_assert(!Tr::kRowNC || 512 % BM == 0, "N-contiguous panel rows must tile 1 KiB");
-    static_assert(!Tr::kColNC || 512 % BN == 0, "N-contiguous panel rows must tile 1 KiB");
+    static_assert(!Tr::kRowNC || BM % 64 == 0, "N-contiguous panel rows of whole 128 B");
+    static_assert(!Tr::kColNC || BN % 64 == 0, "N-contiguous panel rows of whole 128 B");
 
     constexpr int kStages = Geo::kStages;
     // Apply stages: a·X is added into the accumulators at the K-steps whose operand
@@ -186,16 +185,19 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // chunk's row/column lies outside the matrix).
     // K-contiguous panel ([rows][64], 8 rows per 1 KiB instruction) or
     // N-contiguous panel ([64][rows], 512 / rows K-rows per instruction).
-    constexpr int kARowsPerInstr = 512 / BM, kALanesPerRow = BM / 8;
-    constexpr int kBRowsPerInstr = 512 / BN, kBLanesPerRow = BN / 8;
+    // N-contiguous panels [64][rows]: 16-byte chunk q of the panel (q = 64 * DMA
+    // instruction + lane, row-major) is K-row q / (rows / 8), position q % (rows / 8).
+    constexpr int kAChunksPerKRow = BM / 8, kBChunksPerKRow = BN / 8;
     auto a_row = [&](int i) { return 8 * (wave * Geo::kLoadsA + i) + (lane >> 3); };
     auto a_chunk = [&](int i) { return (lane & 7) ^ kc_swz(a_row(i)); };
     auto a_krow = [&](int i) {  // N-contiguous row operand
-        return (wave * Geo::kLoadsA + i) * kARowsPerInstr + lane / kALanesPerRow;
+        return ((wave * Geo::kLoadsA + i) * 64 + lane) / kAChunksPerKRow;
     };
+    auto a_kpos = [&](int i) { return ((wave * Geo::kLoadsA + i) * 64 + lane) % kAChunksPerKRow; };
     auto b_krow = [&](int i) {  // N-contiguous column operand
-        return (wave * Geo::kLoadsB + i) * kBRowsPerInstr + lane / kBLanesPerRow;
+        return ((wave * Geo::kLoadsB + i) * 64 + lane) / kBChunksPerKRow;
     };
+    auto b_kpos = [&](int i) { return ((wave * Geo::kLoadsB + i) * 64 + lane) % kBChunksPerKRow; };
     auto b_row = [&](int i) { return 8 * (wave * Geo::kLoadsB + i) + (lane >> 3); };
     auto b_chunk = [&](int i) { return (lane & 7) ^ kc_swz(b_row(i)); };
 
@@ -204,7 +206,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     for (int i = 0; i < Geo::kLoadsA; ++i) {
         if constexpr (Tr::kRowNC) {
             const int krow = a_krow(i);
-            const int c = (lane % kALanesPerRow) ^ nc_swz<BM>(krow);
+            const int c = a_kpos(i) ^ nc_swz<BM>(krow);
             const int col = row0 + 8 * c;
             off_a[i] =
                 col < g.row_rows ? static_cast<uint32_t>((krow * g.ld_row + col) * 2) : kOob;
@@ -219,7 +221,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     for (int i = 0; i < Geo::kLoadsB; ++i) {
         if constexpr (Tr::kColNC) {
             const int krow = b_krow(i);
-            const int c = (lane % kBLanesPerRow) ^ nc_swz<BN>(krow);
+            const int c = b_kpos(i) ^ nc_swz<BN>(krow);
             const int col = col0 + 8 * c;
             off_b[i] =
                 col < g.col_rows ? static_cast<uint32_t>((krow * g.ld_col + col) * 2) : kOob;
@@ -972,7 +974,7 @@ const void *kernel_by_tile(int bm, int bn, int waves, int depth) {
     if (bm == 64 && bn == 64) return kernel_for<64, 64, S, KT>(waves, depth);
     if (bm == 128 && bn == 128) return kernel_for<128, 128, S, KT>(waves, depth);
     if (bm == 256 && bn == 256) return kernel_for<256, 256, S, KT>(waves, depth);
-    if constexpr (S == Stage::Gram || S == Stage::Poly) {
+    if constexpr (S == Stage::Gram || S == Stage::Poly || S == Stage::GramT) {
         if (bm == 192 && bn == 192) return kernel_for<192, 192, S, KT>(waves, depth);
     }
     if constexpr (!StageTraits<S>::kSymmetric) {

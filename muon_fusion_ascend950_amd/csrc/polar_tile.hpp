@@ -65,11 +65,17 @@ __device__ __forceinline__ int kc_offset(int row, int chunk) {
 // 2 chunks (32 B) per 16-lane group, and a half-wave (two groups: 16 adjacent
 // columns each) is served per LDS cycle.  Rows are 2*BN bytes apart, a multiple
 // of the 256-byte bank window, so without the XOR all 4 rows would share banks.
-// XOR by 4*(k%4) (BN >= 128) puts the half-wave's 16 chunks on 16 distinct
+// XOR by 4*(k%4) (BN = 128, 256) puts the half-wave's 16 chunks on 16 distinct
 // positions of the window: no bank conflict.  BN = 64 rows have 8 chunks only;
-// XOR by 2*(k%4) there (two groups then share banks).
+// XOR by 2*(k%4) there (two groups then share banks).  BN = 192: rows are 384 B
+// apart, so rows k and k+1 already sit half a window apart and rows k and k+2
+// share banks; XOR by 4 on rows with bit 1 of k set (the half-wave's 4
+// consecutive chunks start at a multiple of 4) moves rows k+2, k+3 onto the
+// other half of each 8-chunk group: 16 distinct positions, and the XOR keeps
+// every position inside its row of 24 chunks.
 template <int BN>
 __device__ __forceinline__ int nc_swz(int krow) {
+    if constexpr (BN == 192) return ((krow >> 1) & 1) << 2;
     return BN >= 128 ? (krow & 3) << 2 : (krow & 3) << 1;
 }
 template <int BN>

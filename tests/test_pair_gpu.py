@@ -162,3 +162,18 @@ def test_stage_calls_equal_the_unsplit_step(monkeypatch, shape):
     assert torch.equal(gram.view(torch.uint8).reshape(-1), ws[:gram_bytes])
     assert torch.equal(poly.view(torch.uint8).reshape(-1), ws[p_off:p_off + gram_bytes])
     assert torch.equal(y, y_step)
+
+
+@pytest.mark.parametrize("shape", [(1, 14336, 4096), (2, 1000, 600), (1, 700, 200)])
+def test_right_gram_pairs_equal_transposed_path(monkeypatch, shape):
+    """The right-Gram form's 192x192 pairs (X columns as the N-contiguous operand, read
+    transposed) sum the same products in the same two chains as the left form's pairs
+    on the transposed input: unsplit, bit for bit."""
+    _set(monkeypatch, PAIRS)
+    monkeypatch.setenv("MUON_POLAR_STREAM_K", "0")
+    x = O.make_input(shape, seed=36).to(DEV)
+    print(f"right-Gram pairs {shape}", flush=True)
+    y = torch.ops.muon_ascend950.polar_step_tall(x, *C0)
+    yt = torch.ops.muon_ascend950.polar_step(x.mT.contiguous(), *C0).mT.contiguous()
+    torch.cuda.synchronize()
+    assert torch.equal(y, yt)

@@ -68,30 +68,24 @@ def test_other_plans_store_inside_their_buffers(shape, occ):
 
 @pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)])
 def test_headline_plan(shape):
-    """The walk covers the stream-K path: at [4096,14336] with one 256x256
-    workgroup per CU apply cuts its last round; gram and poly run one round of
-    192x192 tiles (253 on 256 CUs, 8-wave wave-pair kernels), so A and P are padded
-    to 4224 rows.  The right-Gram form ([14336,4096]) keeps 256x256 gram tiles, all
-    136 cut by stream-K, and writes zeros past its 4096-row tile grid."""
+    """At [4096,14336] and in the right-Gram form at [14336,4096], with one
+    workgroup per CU: gram and poly run one round of 192x192 tiles (253 on 256
+    CUs, 8-wave wave-pair kernels, three ring slots), so A and P are padded to
+    4224 rows; apply runs three rounds of whole 256x256 tiles and its last 128
+    tiles as 256 column halves (no stream-K partials anywhere)."""
     plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(1, 1, 1))
     check(plan)
-    tall = shape[1] > shape[2]
     apply = plan.stage[2]
     assert (apply.tile_m, apply.tile_n, apply.waves) == (256, 256, 8)
-    assert apply.total_tiles == 896 and apply.dp_tiles == 768 and apply.sk_units > 0
-    poly = plan.stage[1]
-    assert (poly.tile_m, poly.tile_n, poly.waves, poly.total_tiles, poly.sk_units) == (
-        192, 192, 8, 253, 0)
-    gram = plan.stage[0]
-    if tall:
-        assert (gram.tile_m, gram.tile_n, gram.waves) == (256, 256, 8)
-        # 136 upper tiles, all in the split
-        assert gram.total_tiles == 136 and gram.dp_tiles == 0 and gram.sk_units > 0
-    else:
-        assert (gram.tile_m, gram.tile_n, gram.waves, gram.total_tiles, gram.sk_units) == (
-            192, 192, 8, 253, 0)
-    # A reaches its last byte: gram's zeros past its grid (tall) or its last tile row
-    assert gram.out_hi == gram.out_limit == 4224 * 4224 * 2
+    assert apply.total_tiles == 896 and apply.dp_tiles == 768
+    assert apply.halves == 1 and apply.sk_units == 256
+    for s in (0, 1):
+        e = plan.stage[s]
+        assert (e.tile_m, e.tile_n, e.waves, e.depth, e.total_tiles, e.sk_units) == (
+            192, 192, 8, 3, 253, 0)
+    # A reaches its last byte: gram's last tile row ends at the padded extent
+    assert plan.stage[0].out_hi == plan.stage[0].out_limit == 4224 * 4224 * 2
+    assert plan.partials_offset == plan.pad_offset  # no partial slots
 
 
 @pytest.mark.parametrize("gram,poly", [(256, 192), (192, 256), (64, 192), (192, 128), (128, 64)])

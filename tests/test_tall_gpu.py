@@ -29,15 +29,16 @@ import torch
 
 from oracle import polar_oracle as O
 from tests.test_polar_step_gpu import assert_close_kernels, assert_matches_oracle, bits
-from tests.test_stream_k_gpu import EXACT_COEFFS, assert_bits_equal, split_in_use
+from tests.test_stream_k_gpu import EXACT_COEFFS, HEADLINE_SPLIT, assert_bits_equal, split_in_use
 
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 C0 = O.COEFFICIENTS[0]
-# (batch, M, N), M > N, N % 8 == 0: the headline shape transposed (all three stages
-# split), ragged M and N (edge tiles, padded Gram rows, partial last K-step), small N
-# (64-row tiles), batch.
+# (batch, M, N), M > N, N % 8 == 0: the headline shape transposed (192x192 wave
+# pairs for G and P, apply's last round as column halves; split on every stage with
+# HEADLINE_SPLIT), ragged M and N (edge tiles, padded Gram rows, partial last
+# K-step), small N (64-row tiles), batch.
 TALL_SHAPES = [(1, 14336, 4096), (2, 700, 256), (3, 523, 200), (1, 4100, 1000), (4, 2048, 64)]
 
 
@@ -81,11 +82,14 @@ def test_unsplit_equals_transposed_path_bitwise(monkeypatch, shape):
 
 
 @pytest.mark.parametrize("split", ["1", "0"])
-@pytest.mark.parametrize("shape", [(1, 14336, 4096), (3, 523, 200), (2, 8192, 768)])
-def test_exact_sums_are_bitwise(monkeypatch, shape, split):
+@pytest.mark.parametrize("shape,env", [((1, 14336, 4096), {}), ((1, 14336, 4096), HEADLINE_SPLIT),
+                                       ((3, 523, 200), {}), ((2, 8192, 768), {})])
+def test_exact_sums_are_bitwise(monkeypatch, shape, env, split):
     monkeypatch.setenv("MUON_POLAR_STREAM_K", split)
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
     batch, m, n = shape
-    if split == "1" and shape[1] >= 8192:
+    if split == "1" and (env or shape[0] == 2):
         assert split_in_use(*shape)
     capi = _capi()
     mats = O.sparse_sign_input(shape, 16, seed=32)
@@ -114,9 +118,12 @@ def test_exact_sums_are_bitwise(monkeypatch, shape, split):
         assert_bits_equal(bits(y[i]), O.f32_to_bf16_bits(yt_ref.T.astype(np.float32)), "Y")
 
 
-@pytest.mark.parametrize("shape", [(1, 14336, 4096), (2, 8192, 768)])
-def test_split_is_deterministic_and_close_to_transposed(shape):
-    assert split_in_use(*shape)
+@pytest.mark.parametrize("shape,env", [((1, 14336, 4096), HEADLINE_SPLIT),
+                                       ((1, 14336, 4096), {}), ((2, 8192, 768), {})])
+def test_split_is_deterministic_and_close_to_transposed(monkeypatch, shape, env):
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    assert split_in_use(*shape) == (env != {} or shape[0] == 2)
     print(f"split tall {shape}", flush=True)
     x = O.make_input(shape, seed=34).to(DEV)
     first = step_tall(x, *C0)
