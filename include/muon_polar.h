@@ -29,6 +29,12 @@
  * the launch that wrote it, and words of other launches count as zero, so the
  * workspace needs no clearing (any content, graph replays included).  Calls that
  * share one workspace must not overlap (use one workspace per concurrent stream).
+ * Stage 3 with 256x256 tiles instead runs such a last round, when it holds
+ * between a quarter and a half of the resident workgroups, as 256x128 column
+ * halves in the same launch (whole K each; no partials, no counters).  Results
+ * of the 192x192 tiles with 8 waves and of those halves sum each output's K
+ * terms in two interleaved chains (wave pairs): they equal the one-chain kernels
+ * to fp32 rounding.
  *
  * Rows of n % 8 != 0 elements: each step first copies X into a zero-padded
  * [batch, m, roundup(n, 64)] buffer at the end of the workspace, so that the
