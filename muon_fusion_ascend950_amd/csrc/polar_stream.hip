@@ -440,6 +440,9 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // slot instead; every later wait lets those loads stay in flight.
     const int nkl = kend - kbeg;
     constexpr bool kEpiPrefetch = kEpiLoad && Geo::kEpiInSlot;
+    // The wave pairs add their halves through the ring after the K loop, which
+    // would overwrite an epilogue tile fetched into a ring slot during the loop.
+    static_assert(!(kPair && kEpiPrefetch), "wave pairs cannot prefetch the epilogue tile");
     const int npro = nkl < kStages ? nkl : kStages;
     for (int i = 0; i < npro; ++i) issue_all(kbeg + i, i);
     int epi_slot = 0;
