@@ -143,3 +143,25 @@ def test_rows_of_whole_chunks_are_read_in_place(shape):
     plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(1, 1, 1))
     assert plan.pad_end == 0
     check(plan)
+
+
+def _random_shapes(count: int, seed: int):
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        b = int(rng.integers(1, 17))
+        short = int(rng.integers(1, 4097))
+        long = int(rng.integers(short, 16385))
+        out.append((b, short, long) if rng.random() < 0.6 else (b, long, short))
+    return out
+
+
+@pytest.mark.parametrize("shape", _random_shapes(200, seed=7), ids=lambda s: "x".join(map(str, s)))
+def test_random_plans_store_inside_their_buffers(shape):
+    """Seeded random shapes (batch 1-16, sides up to 16384, wide and tall): every
+    stage's walk stays inside its buffers and computes each iteration once, at the
+    occupancies the kernels can report."""
+    for occ in [(1, 1, 1), (2, 2, 2), (1, 2, 2)]:
+        check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
