@@ -205,7 +205,8 @@ typedef struct muon_polar_stage_extent {
     int32_t extents_ok;    /* per-matrix operand byte extents < 2^31 and passed unchanged */
     int32_t halves;        /* 1: tiles past dp_tiles run as sk_units column halves, each over
                               the whole K range (no partial slots, no arrival words) */
-    int32_t reserved;
+    int32_t diag_pairs;    /* 1 (gram, poly): the units are the off-diagonal tiles and pairs of
+                              diagonal tiles (two 64x64 tiles per workgroup, never cut) */
     int64_t out_lo, out_hi, out_limit;          /* output stores, bytes: [lo, hi) vs buffer size */
     int64_t partial_lo, partial_hi, partial_limit; /* stream-K partial slots, bytes */
     int64_t counter_hi, counter_limit;          /* stream-K arrival words used vs reserved */

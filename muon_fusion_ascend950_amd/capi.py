@@ -46,7 +46,7 @@ class ShapeInfo(ctypes.Structure):
 class StageExtent(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "tile_m", "tile_n", "waves", "depth", "dma_fed", "k_steps", "total_tiles", "dp_tiles",
-        "sk_units", "grid", "coverage_ok", "extents_ok", "halves", "reserved")] + [
+        "sk_units", "grid", "coverage_ok", "extents_ok", "halves", "diag_pairs")] + [
         (name, ctypes.c_int64) for name in (
             "out_lo", "out_hi", "out_limit", "partial_lo", "partial_hi", "partial_limit",
             "counter_hi", "counter_limit")]

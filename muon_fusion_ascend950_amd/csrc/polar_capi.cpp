@@ -65,12 +65,14 @@ struct Knobs {
     uint32_t pair;      // 1: 192x192 tiles run the 8-wave wave-pair kernels when waves == 8
     uint32_t halves;    // 1: apply's last round as 256x128 halves where it fits (below)
     uint32_t halves_depth;  // LDS ring slots of those halves (2 or 3)
+    uint32_t diag_pairs;    // 1: triangular stages pair their diagonal tiles where it
+                            // takes fewer rounds of workgroups (below)
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
                apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k &&
                waves == o.waves && depth[0] == o.depth[0] && depth[1] == o.depth[1] &&
                depth[2] == o.depth[2] && pair == o.pair && halves == o.halves &&
-               halves_depth == o.halves_depth;
+               halves_depth == o.halves_depth && diag_pairs == o.diag_pairs;
     }
 };
 
@@ -104,6 +106,7 @@ struct PlanKeyHash {
         mix(k.knobs.pair);
         mix(k.knobs.halves);
         mix(k.knobs.halves_depth);
+        mix(k.knobs.diag_pairs);
         return static_cast<size_t>(h);
     }
 };
@@ -135,6 +138,9 @@ struct Plan {
     // after A and P: arrival words (counter_stride 64-bit words per stage), then
     // the fp32 partial slots shared by the three stages.
     SkSplit sk[3];
+    // gram and poly: the DMA-fed kernel runs the off-diagonal tiles and pairs of
+    // diagonal tiles as its units (GemmArgs::diag_pairs; never split)
+    bool diag[2];
     bool sk_any;
     int64_t counter_stride;
     size_t counters_offset, partials_offset;
@@ -228,6 +234,8 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     if (k.halves > 2) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_APPLY_HALVES must be 0, 1 or 2");
     // three 48 KiB slots for the halves: [4096,14336] apply 395 -> 390 us
     k.halves_depth = static_cast<uint32_t>(env_u64("MUON_POLAR_HALVES_DEPTH", 3));
+    k.diag_pairs = static_cast<uint32_t>(env_u64("MUON_POLAR_DIAG_PAIRS", 1));
+    if (k.diag_pairs > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_DIAG_PAIRS must be 0 or 1");
     if (k.halves_depth != 2 && k.halves_depth != 3)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_HALVES_DEPTH must be 2 or 3");
     // Gram takes 192x192 tiles where poly does (one round of them fills the CUs,
@@ -404,6 +412,19 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
                         "others: 2)");
     }
     for (int s = 0; s < 3; ++s) {
+        // Gram and poly on 64x64 tiles: pair the diagonal tiles when that takes
+        // fewer rounds of one workgroup per CU, and then run unsplit ([8,512,2048]:
+        // 288 tiles -> 256 units, one per CU, where 32 CUs ran two tiles).
+        if (s < 2 && knobs.diag_pairs != 0 && p.stream && cus > 0 && tiles_bm[s] == 64 &&
+            tiles_bn[s] == 64 && p.waves[s] == 4) {
+            const int nt = s == 0 ? p.gram_nt : p.poly_nt;
+            const int64_t units = batch * muon_polar::sym_units(nt, true);
+            if (nt >= 2 && ceil_div(units, cus) < ceil_div(grids[s], cus)) {
+                p.diag[s] = true;
+                p.sk[s] = SkSplit{units, 0, 0, 0};
+                continue;
+            }
+        }
         const bool sk_stage = sk_ok && (knobs.stream_k >> s & 1u) != 0;
         int occ = 0;
         if (sk_stage)
@@ -781,6 +802,11 @@ void prepare_stage(StageLaunch &L, int64_t batch, const Plan &p, const SkArea *a
     g.bytes_row = static_cast<uint32_t>(L.extent[0]);
     g.bytes_col = static_cast<uint32_t>(L.extent[1]);
     g.bytes_epi = static_cast<uint32_t>(L.extent[2]);
+    g.diag_pairs = 0;
+    if (L.stream_ok && L.sk_index < 2 && p.diag[L.sk_index]) {
+        g.diag_pairs = 1;
+        g.tiles_per_batch = muon_polar::sym_units(g.tiles_m, true);
+    }
     g.total_tiles = static_cast<int32_t>(batch * g.tiles_per_batch);
     g.k_steps = g.k_loop / 64;
     g.dp_tiles = g.total_tiles;
@@ -935,7 +961,7 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
     e.dp_tiles = g.dp_tiles;
     e.sk_units = g.sk_units;
     e.halves = g.halves != 0 ? 1 : 0;
-    e.reserved = 0;
+    e.diag_pairs = g.diag_pairs;
     e.grid = L.stream_ok ? g.sk_units + 8 * g.per_xcd : static_cast<int32_t>(L.grid);
     e.out_lo = INT64_MAX;
     e.out_hi = 0;
@@ -982,6 +1008,18 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
         }
         e.out_lo = std::min(e.out_lo, lo * 2);
         e.out_hi = std::max(e.out_hi, hi * 2);
+    };
+    // Triangular stages on the DMA-fed kernels: every upper tile of every batch
+    // matrix started by exactly one workgroup (units may hold two diagonal tiles).
+    const int64_t nbatch = g.tiles_per_batch > 0 ? g.total_tiles / g.tiles_per_batch : 0;
+    const int ntm = sym ? g.tiles_m : 0;
+    std::vector<uint8_t> tile_seen(static_cast<size_t>(nbatch) * ntm * ntm, 0);
+    auto mark_tile = [&](int bt, int tm, int tn) {
+        if (bt < 0 || bt >= nbatch || tm < 0 || tn < tm || tn >= ntm) {
+            once = false;
+            return;
+        }
+        ++tile_seen[(size_t(bt) * ntm + tm) * ntm + tn];
     };
     if (!L.stream_ok) {
         // register-staged kernels: one workgroup per tile
@@ -1051,9 +1089,22 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
                 }
                 for (int k = kbeg; k < kend; ++k) once = once && seen[size_t(tlin) * nk + k]++ == 0;
                 const int bt = tlin / g.tiles_per_batch;
+                const int t = tlin - bt * g.tiles_per_batch;
                 int tm, tn;
-                muon_polar::tile_coords(g, sym, tlin - bt * g.tiles_per_batch, tm, tn);
-                store_tile(bt, tm * L.bm, tn * L.bn, L.bn);
+                muon_polar::tile_coords(g, sym, t, tm, tn);
+                const bool pair = sym && muon_polar::is_diag_pair(g, t);
+                if (pair) {
+                    // the two diagonal tiles (tm, tm) and (tn, tn) = (tm + 1, tm + 1)
+                    store_tile(bt, tm * L.bm, tm * L.bn, L.bn);
+                    store_tile(bt, tn * L.bm, tn * L.bn, L.bn);
+                    if (kbeg != 0 || kend != nk) once = false;  // pairs are never cut
+                } else {
+                    store_tile(bt, tm * L.bm, tn * L.bn, L.bn);
+                }
+                if (sym && kbeg == 0) {
+                    mark_tile(bt, tm, pair ? tm : tn);
+                    if (pair) mark_tile(bt, tn, tn);
+                }
                 if (kbeg != 0 || kend != nk) {
                     // cut tile: arrival word lt, partial slots of its contributors
                     if (!splits || unit < 0) {
@@ -1074,6 +1125,11 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
         }
     }
     for (uint8_t c : seen) once = once && c == 1;
+    if (sym && L.stream_ok && !g.halves)
+        for (int64_t bt = 0; bt < nbatch; ++bt)
+            for (int tm = 0; tm < ntm; ++tm)
+                for (int tn = tm; tn < ntm; ++tn)
+                    once = once && tile_seen[(size_t(bt) * ntm + tm) * ntm + tn] == 1;
     e.coverage_ok = once ? 1 : 0;
     if (e.out_lo == INT64_MAX) e.out_lo = 0;
     if (e.partial_lo == INT64_MAX) e.partial_lo = 0;

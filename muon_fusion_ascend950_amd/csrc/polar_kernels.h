@@ -76,6 +76,14 @@ struct GemmArgs {
     // whole tiles, with that many ring slots, sk_units = the number of halves (no
     // partials, no arrival words); 0 = the stream-K split above.
     int32_t halves;
+    // Triangular stages (DMA-fed, 64x64 tiles with 4 waves, no stream-K split):
+    // 1 = the tiles_per_batch units of a batch matrix are its tiles_m (tiles_m - 1)
+    // / 2 off-diagonal tiles (the super-block walk without the diagonal), then
+    // (tiles_m + 1) / 2 diagonal units, unit p holding the diagonal tiles 2p and
+    // 2p + 1 (2p alone when it is the last), so that fewer workgroups run the
+    // same tiles (diagonal tiles read one panel each; a pair reads the two panels
+    // an off-diagonal tile reads).  0 = every upper tile a unit of its own.
+    int32_t diag_pairs;
 };
 
 bool tile_supported(Stage s, int bm, int bn);

@@ -64,12 +64,73 @@ __host__ __device__ __forceinline__ void upper_tile_blocked(int t, int nt, int b
     }
 }
 
+// The off-diagonal tiles (tn > tm) in the order of upper_tile_blocked with the
+// diagonal tiles left out.
+__host__ __device__ __forceinline__ void strict_upper_tile_blocked(int t, int nt, int b, int &tm,
+                                                                   int &tn) {
+    if (b <= 1) b = nt;  // row by row: one super-block
+    const int ns = (nt + b - 1) / b;
+    tm = tn = 0;
+    for (int bi = 0; bi < ns; ++bi) {
+        const int rows = b < nt - bi * b ? b : nt - bi * b;
+        const int above = rows * (rows - 1) / 2;
+        if (t < above) {
+            int r = 0, len = rows - 1;
+            while (t >= len) {
+                t -= len;
+                ++r;
+                --len;
+            }
+            tm = bi * b + r;
+            tn = bi * b + r + 1 + t;
+            return;
+        }
+        t -= above;
+        for (int bj = bi + 1; bj < ns; ++bj) {
+            const int cols = b < nt - bj * b ? b : nt - bj * b;
+            if (t < rows * cols) {
+                tm = bi * b + t / cols;
+                tn = bj * b + t % cols;
+                return;
+            }
+            t -= rows * cols;
+        }
+    }
+}
+
+// Units of one batch matrix of a triangular stage (g.diag_pairs: off-diagonal
+// tiles, then diagonal pairs; else its upper tiles).
+__host__ __device__ __forceinline__ int sym_units(int nt, bool diag_pairs) {
+    return diag_pairs ? nt * (nt - 1) / 2 + (nt + 1) / 2 : nt * (nt + 1) / 2;
+}
+
+// Whether unit t of a batch matrix is a pair of diagonal tiles (2p, 2p) and
+// (2p + 1, 2p + 1); tile_coords gives it (tm, tn) = (2p, 2p + 1), the tile whose
+// row and column panels are the two tiles' panels.
+__host__ __device__ __forceinline__ bool is_diag_pair(const GemmArgs &g, int t) {
+    if (!g.diag_pairs) return false;
+    const int off = g.tiles_m * (g.tiles_m - 1) / 2;
+    return t >= off && 2 * (t - off) + 1 < g.tiles_m;
+}
+
 // Tile (tm, tn) of linear tile t of one batch matrix.  Triangular stages: the
-// super-block walk above.  Others: runs of group_n column tiles walked row by
-// row, so the tiles an XCD holds at once share few row- and column-operand panels.
+// super-block walk above (with g.diag_pairs, the unit order above: a diagonal
+// pair gives (2p, 2p + 1), a last diagonal tile alone (2p, 2p)).  Others: runs
+// of group_n column tiles walked row by row, so the tiles an XCD holds at once
+// share few row- and column-operand panels.
 __host__ __device__ __forceinline__ void tile_coords(const GemmArgs &g, bool symmetric, int t,
                                                      int &tm, int &tn) {
     if (symmetric) {
+        if (g.diag_pairs) {
+            const int off = g.tiles_m * (g.tiles_m - 1) / 2;
+            if (t < off) {
+                strict_upper_tile_blocked(t, g.tiles_m, g.group_n, tm, tn);
+            } else {
+                tm = 2 * (t - off);
+                tn = tm + 1 < g.tiles_m ? tm + 1 : tm;
+            }
+            return;
+        }
         upper_tile_blocked(t, g.tiles_m, g.group_n, tm, tn);
         return;
     }

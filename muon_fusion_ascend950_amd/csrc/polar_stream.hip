@@ -109,8 +109,9 @@ __device__ __forceinline__ int epi_offset(int row, int col) {
 // LDS: the ring of D K-step slots, the per-wave DMA sink and one arrival word.
 // half >= 0: the segment computes column half `half` (BN wide) of the tile of
 // the launch's 2*BN-wide tile grid (the apply stage's last round, see
-// polar_stream_halves_kernel).
-template <int BM, int BN, Stage S, int NW, int D, bool KT>
+// polar_stream_halves_kernel).  DG: the unit is a pair of diagonal tiles
+// (GemmArgs::diag_pairs; tile (tm, tn) = (2p, 2p + 1) names its two panels).
+template <int BM, int BN, Stage S, int NW, int D, bool KT, bool DG = false>
 __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem, uint16_t *sink,
                                                uint32_t *s_arrived_p, int unit, int tile_base,
                                                int lt, int kbeg, int kend, int half = -1) {
@@ -128,7 +129,19 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // rounding from the single-chain kernels.
     constexpr bool kPair = NW == 8 && ((BM == 192 && BN == 192) || (BM == 256 && BN == 128));
     constexpr int kGridWaves = kPair ? 4 : NW;
-    constexpr int WM = BM / 2, WN = BN / (kGridWaves / 2);
+    // Diagonal pairs (DG, 64x64 tiles with 4 waves): waves 0-1 compute diagonal
+    // tile 2p from the row panel, waves 2-3 tile 2p + 1 from the column panel.
+    // Of a tile's 32x32 blocks the store needs (0,0), (0,1) and (1,1): wave h
+    // (= w & 1) sums its diagonal block (h,h) over every k16 slice and the shared
+    // block over its two slices of each K-step (h = 0: block (0,1) over slices
+    // 0-1; h = 1: block (1,0), the transpose, over slices 2-3), which h = 0 adds
+    // in transposed after the K loop.  Six MFMAs and six fragment reads per wave
+    // and K-step, against four and eight for an off-diagonal tile.  Block (0,1)
+    // then sums its K terms in two interleaved chains and wave 1 takes its slices
+    // in the order 2, 3, 0, 1: results differ in rounding from single tiles.
+    static_assert(!DG || (StageTraits<S>::kSymmetric && BM == 64 && BN == 64 && NW == 4),
+                  "diagonal pairs: 64x64 tiles of a triangular stage, 4 waves");
+    constexpr int WM = BM / 2, WN = DG ? BN : BN / (kGridWaves / 2);
     constexpr int SM = WM / 32, SN = WN / 32;
     constexpr int kMfmaPerSlice = SM * SN;
     // Threads that hold accumulators (the h = 0 waves in pair mode).
@@ -152,12 +165,19 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     constexpr bool kBigAcc = (BM / 2) * (BN / (NW / 2)) >= 128 * 128;
     constexpr bool kAxInLoop = Tr::kEpilogue == Stage::Apply && !kBigAcc;
     constexpr bool kEpiLoad = Tr::kEpiOperand && !kAxInLoop;
+    // DMA instructions per wave of the epilogue operand tile (two tiles for a
+    // diagonal pair, which fill one ring slot)
+    constexpr int kEpiLoadsU = DG ? 2 * Geo::kEpiLoads : Geo::kEpiLoads;
+    static_assert(!DG || 2 * Geo::kTileBytes <= Geo::kStageBytes, "a pair's tiles fill one slot");
+    static_assert((D - 1) * Geo::kLoads + kEpiLoadsU <= 63, "vmcnt range");
     // Fragment schedule: a whole K-step ahead for one MFMA per slice, else one slice.
     constexpr bool kStepFrags = kMfmaPerSlice == 1;
     uint32_t &s_arrived = *s_arrived_p;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int wq = kPair ? (wave & 3) : wave;  // wave tile of this wave
-    const int wr = wq & 1, wc = wq >> 1;
+    const int wr = wq & 1, wc = DG ? 0 : wq >> 1;
+    const int dt = DG ? wave >> 1 : 0;  // diagonal pairs: this wave's tile of the two
+    const int hr = DG ? wave & 1 : 0;   // and its row half
     const int kh = kPair ? (wave >> 2) : 0;    // pair mode: which half of the slices
     const bool acc_owner = !kPair || kh == 0;  // holds the tile's sums after the K loop
     const int nk = g.k_steps;
@@ -283,20 +303,25 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
 
     // Epilogue operand tile (A for poly, X for apply) -> LDS ring slot `eslot`
     // (the tile may span several slots from slot 0), rows/cols outside the
-    // matrix read as zero.
+    // matrix read as zero.  Diagonal pairs: both tiles, the second 8 KiB after
+    // the first.
     auto issue_epi = [&](int eslot) {
         if constexpr (kEpiLoad) {
             const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
             constexpr int kChunksPerRow = BN / 8;
+            constexpr int kTileChunks = BM * kChunksPerRow;
 #pragma unroll
-            for (int d = 0; d < Geo::kEpiLoads; ++d) {
+            for (int d = 0; d < kEpiLoadsU; ++d) {
                 // LDS chunk q of the tile (row q / kChunksPerRow, position q %
                 // kChunksPerRow) receives global chunk epi_pos(row, position).
-                const int blk = wave * Geo::kEpiLoads + d;
-                const int q = blk * 64 + lane;
+                const int blk = wave * kEpiLoadsU + d;
+                const int qt = blk * 64 + lane;
+                const int et = DG ? qt / kTileChunks : 0;  // which tile of a pair
+                const int q = DG ? qt - et * kTileChunks : qt;
                 const int row = q / kChunksPerRow;
                 const int c = epi_pos<BN>(row, q - row * kChunksPerRow);
-                const int gr = row0 + row, gc = col0 + 8 * c;
+                const int er0 = DG ? row0 + et * BM : row0, ec0 = DG ? er0 : col0;
+                const int gr = er0 + row, gc = ec0 + 8 * c;
                 const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
                                        ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
                                        : kOob;
@@ -450,7 +475,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
         if (nkl < kStages) {
             epi_slot = nkl;  // a slot the K loop never fills
             issue_epi(epi_slot);
-            wait_panels_barrier<Geo::kLoads, kStages, Geo::kEpiLoads>(npro - 1);
+            wait_panels_barrier<Geo::kLoads, kStages, kEpiLoadsU>(npro - 1);
         } else {
             epi_slot = (nkl - kStages) % kStages;
             wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
@@ -480,7 +505,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             // the waits of the schedule below (panel k+1; later DMA groups in flight)
             const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
             if (kEpiPrefetch && k > nkl - kStages)
-                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
+                wait_panels_barrier<Geo::kLoads, kStages - 1, kEpiLoadsU>(after);
             else
                 wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
             mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
@@ -491,6 +516,65 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             }
             slot = next;
         }
+    } else if constexpr (DG) {
+        // Fragments of one K-step, slices taken in the order s_i = (2h + i) mod 4:
+        // o[i] = rows 32h.. (own block), t[i] = rows 32(1-h).. (shared block, i < 2).
+        bf16x8 ao[4], at[2], bo[4], bt[2];
+        auto frag_of = [&](const uint16_t *ps, int rbase, int kk) {
+            if constexpr (Tr::kRowNC)
+                return frag_nc_tr<BM>(ps, rbase + ((lane >> 4) & 1) * 16, kk, lane);
+            else
+                return frag_kc(ps, rbase + (lane & 31), kk, lane);
+        };
+        auto read_dg = [&](int sl, bf16x8 (&o)[4], bf16x8 (&t)[2]) {
+            const uint16_t *ps = smem + sl * (Geo::kStageBytes / 2) + dt * (Geo::kABytes / 2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kk = (2 * hr + i) & 3;
+                o[i] = frag_of(ps, 32 * hr, kk);
+                if (i < 2) t[i] = frag_of(ps, 32 - 32 * hr, kk);
+            }
+        };
+        auto step_dg = [&](int k, const bf16x8 (&o)[4], const bf16x8 (&t)[2], bf16x8 (&no)[4],
+                           bf16x8 (&nt)[2]) {
+            const int next = slot + 1 == kStages ? 0 : slot + 1;
+            // the waits of the one-MFMA-per-slice schedule below
+            const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+            if (kEpiPrefetch && k > nkl - kStages)
+                wait_panels_barrier<Geo::kLoads, kStages - 1, kEpiLoadsU>(after);
+            else
+                wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
+            read_dg(next, no, nt);  // stale on the last step, not used
+            __builtin_amdgcn_sched_barrier(0);
+            constexpr int kM = 6;
+            const int dstep = kbeg + k + kStages;
+            const bool live = k + kStages < nkl;
+#pragma unroll
+            for (int m = 0; m < kM; ++m) {
+                // m = 0..5: own(0), shared(0), own(1), shared(1), own(2), own(3)
+                const int i = m < 4 ? m >> 1 : m - 2;
+                if (m < 4 && (m & 1))
+                    acc[0][1] = mfma_32x32x16(t[i & 1], o[i], acc[0][1]);
+                else
+                    acc[0][0] = mfma_32x32x16(o[i], o[i], acc[0][0]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int d = m * Geo::kLoads / kM; d < (m + 1) * Geo::kLoads / kM; ++d)
+                    dma_one(d, dstep, slot, live);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (kEpiPrefetch) {
+                if (k == nkl - kStages) issue_epi(epi_slot);
+            }
+            slot = next;
+        };
+        read_dg(0, ao, at);
+        int k = 0;
+        for (; k + 1 < nkl; k += 2) {
+            step_dg(k, ao, at, bo, bt);
+            step_dg(k + 1, bo, bt, ao, at);
+        }
+        if (k < nkl) step_dg(k, ao, at, bo, bt);
     } else if constexpr (kStepFrags) {
         // One MFMA per k16 slice (32x32 wave tiles): a slice's fragment reads
         // cannot hide behind the single MFMA issued before them, so every slice
@@ -510,7 +594,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             // step's DMA group
             const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
             if (kEpiPrefetch && k > nkl - kStages)
-                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
+                wait_panels_barrier<Geo::kLoads, kStages - 1, kEpiLoadsU>(after);
             else
                 wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
             read_step(next, nr, nc);  // stale on the last step, not used
@@ -583,7 +667,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             // MFMAs would then wait for all of them.
             const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
             if (kEpiPrefetch && k > nkl - kStages)
-                wait_panels_barrier<Geo::kLoads, kStages - 1, Geo::kEpiLoads>(after);
+                wait_panels_barrier<Geo::kLoads, kStages - 1, kEpiLoadsU>(after);
             else
                 wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
             mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
@@ -597,6 +681,32 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     }
     // All waves are done with the ring (and no DMA is outstanding).
     wait_vm_barrier<0>();
+
+    // Diagonal pairs: wave h = 1's block (1,0) over slices 2-3 goes through the ring
+    // ([32][33] floats per tile, in a slot the epilogue tile was not fetched into)
+    // and is added transposed into wave h = 0's block (0,1): (0,1)[r][c] += (1,0)[c][r].
+    if constexpr (DG) {
+        const int red_slot = kEpiPrefetch ? (epi_slot + 1) % kStages : 0;
+        float *red = reinterpret_cast<float *>(smem + red_slot * (Geo::kStageBytes / 2)) +
+                     dt * (32 * 33);
+        static_assert(2 * 32 * 33 * 4 <= Geo::kStageBytes, "pair reduction fits a slot");
+        if (hr == 1) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    red[(lane & 31) * 33 + 8 * q + 4 * (lane >> 5) + e] = acc[0][1][4 * q + e];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (hr == 0) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[0][1][4 * q + e] += red[(8 * q + 4 * (lane >> 5) + e) * 33 + (lane & 31)];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
 
     // Wave pairs: the h = 1 wave's sums are added into its partner's through the
     // ring, in two rounds of accumulator blocks (each round's buffer fits the
@@ -639,7 +749,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
 
     // -------------------------------------------------------- stream-K fixup
     bool epi_issued = false;
-    if (kbeg != 0 || kend != nk) {
+    if (!DG && (kbeg != 0 || kend != nk)) {  // (diagonal pairs are never cut)
         // This tile is cut between units u0 .. u1.  Each contributor but the
         // last stores its fp32 partial and counts itself in; the last one to
         // arrive forms p(u1) + p(u1 - 1) + ... + p(u0) in that fixed order (so
@@ -765,7 +875,8 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // -------------------------------------------------------- epilogue
     uint16_t *tile = smem + epi_slot * (Geo::kStageBytes / 2);
     uint16_t *out = g.out + bt * g.sb_out;
-    const bool diag = Tr::kSymmetric && (tm == tn);
+    const bool diag = Tr::kSymmetric && (DG || tm == tn);
+    constexpr int kOutTiles = DG ? 2 : 1;  // staged [BM][BN] tiles, one after the other
 
     if constexpr (kEpiLoad && !kEpiPrefetch) {
         if (!epi_issued) issue_epi(0);
@@ -782,8 +893,12 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             for (int j = 0; j < SN; ++j) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int c = wc * WN + j * 32 + 8 * q + 4 * (lane >> 5);
-                    u32x2 *p = reinterpret_cast<u32x2 *>(tile + epi_offset<BN>(r, c));
+                    // diagonal pairs: block (h,h), and (0,1) for h = 0
+                    if (DG && hr == 1 && j == 1) continue;
+                    const int cb = DG ? (j == 0 ? 32 * hr : 32) : wc * WN + j * 32;
+                    const int c = cb + 8 * q + 4 * (lane >> 5);
+                    u32x2 *p = reinterpret_cast<u32x2 *>(tile + dt * (BM * BN) +
+                                                         epi_offset<BN>(r, c));
                     float e[4] = {0.f, 0.f, 0.f, 0.f};
                     uint16_t h[4];
                     if constexpr (kAxInLoop) {
@@ -802,15 +917,20 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
 
     // Coalesced store of the tile: 16-byte chunks, consecutive threads along a row.
     constexpr int kChunksPerRow = BN / 8;
-    for (int idx = tid; idx < BM * kChunksPerRow; idx += kThreads) {
-        const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
-        const int gr = row0 + row, gc = col0 + 8 * c;
+    for (int idx = tid; idx < kOutTiles * BM * kChunksPerRow; idx += kThreads) {
+        // diagonal pairs: tile ot of the two at (row0 + ot * BM, row0 + ot * BM)
+        const int ot = DG ? idx / (BM * kChunksPerRow) : 0;
+        const int ti = DG ? idx - ot * (BM * kChunksPerRow) : idx;
+        const int row = ti / kChunksPerRow, c = ti % kChunksPerRow;
+        const int sr0 = DG ? row0 + ot * BM : row0, sc0 = DG ? sr0 : col0;
+        const int gr = sr0 + row, gc = sc0 + 8 * c;
+        const uint16_t *st = tile + ot * (BM * BN);
         if constexpr (!Tr::kSymmetric) {
             if (gr >= g.out_rows || gc >= g.out_cols) continue;
         }
         u32x4 v;
         if (!diag) {
-            v = *reinterpret_cast<const u32x4 *>(tile + epi_offset<BN>(row, 8 * c));
+            v = *reinterpret_cast<const u32x4 *>(st + epi_offset<BN>(row, 8 * c));
         } else {
             // Diagonal tile: element (r, c) comes from the upper-triangle source
             // min/max(r, c), so the stored matrix is bitwise symmetric.
@@ -818,8 +938,8 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int col = 8 * c + e;
-                hh[e] = row <= col ? tile[epi_offset<BN>(row, col)]
-                                   : tile[epi_offset<BN>(col, row)];
+                hh[e] = row <= col ? st[epi_offset<BN>(row, col)]
+                                   : st[epi_offset<BN>(col, row)];
             }
             v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
                       hh[6] | (hh[7] << 16)};
@@ -855,7 +975,12 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
                 *reinterpret_cast<u32x4 *>(out + (col0 + mc) * g.ld_out + row0 + 8 * rb) = v;
             }
         }
-        zero_past_grid<BM>(g, out, tm, tn, tid, kThreads);
+        if constexpr (DG) {
+            zero_past_grid<BM>(g, out, tm, tm, tid, kThreads);
+            zero_past_grid<BM>(g, out, tm + 1, tm + 1, tid, kThreads);
+        } else {
+            zero_past_grid<BM>(g, out, tm, tn, tid, kThreads);
+        }
     }
 }
 
@@ -889,6 +1014,13 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
         const int kbeg = static_cast<int>(lo - tstart), kend = static_cast<int>(hi - tstart);
         if (hi != it_hi) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         hi = lo;
+        if constexpr (StageTraits<S>::kSymmetric && BM == 64 && BN == 64 && NW == 4) {
+            if (is_diag_pair(g, (tile_base + lt) % g.tiles_per_batch)) {
+                stream_segment<BM, BN, S, NW, D, KT, true>(g, smem, sink, &s_arrived, unit,
+                                                           tile_base, lt, kbeg, kend);
+                continue;
+            }
+        }
         stream_segment<BM, BN, S, NW, D, KT>(g, smem, sink, &s_arrived, unit, tile_base, lt, kbeg,
                                          kend);
     }

@@ -52,6 +52,10 @@ def check(plan: capi.PlanExtents) -> None:
             assert e.partial_hi < 2**31
         else:
             assert e.partial_hi == 0 and e.counter_hi == 0
+        if e.diag_pairs:
+            # off-diagonal tiles and pairs of diagonal tiles, never cut
+            assert s < 2 and e.dma_fed == 1 and (e.tile_m, e.tile_n, e.waves) == (64, 64, 4)
+            assert e.sk_units == 0 and e.dp_tiles == e.total_tiles
 
 
 @pytest.mark.parametrize("occ", OCCUPANCIES)
@@ -165,3 +169,48 @@ def test_random_plans_store_inside_their_buffers(shape):
     occupancies the kernels can report."""
     for occ in [(1, 1, 1), (2, 2, 2), (1, 2, 2)]:
         check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
+
+
+def _units(nt: int) -> int:
+    return nt * (nt - 1) // 2 + (nt + 1) // 2
+
+
+@pytest.mark.parametrize("shape", [(8, 512, 2048), (8, 2048, 512), (10, 440, 1024),
+                                   (10, 1024, 440), (10, 448, 1024)])
+@pytest.mark.parametrize("occ", [(1, 1, 1), (2, 2, 2)])
+def test_diagonal_pairs_cover_every_upper_tile_once(shape, occ):
+    """Where pairing the diagonal 64x64 tiles takes fewer rounds of one workgroup per
+    CU (288 tiles -> 256 units at [8,512,2048]; 7 tiles a side leave a last diagonal
+    tile alone), gram and poly run off-diagonal tiles and diagonal pairs, unsplit.
+    The walk checks that every upper tile of every matrix is started by exactly one
+    workgroup and that the stores of both tiles of a pair stay inside A and P."""
+    batch, m, n = shape
+    nt = -(-min(m, n) // 64)
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=occ)
+    check(plan)
+    for s in (0, 1):
+        e = plan.stage[s]
+        assert e.diag_pairs == 1
+        assert e.total_tiles == batch * _units(nt) <= 256
+        assert e.grid == 8 * -(-e.total_tiles // 8)
+
+
+@pytest.mark.parametrize("shape", [(8, 512, 2048), (10, 440, 1024)])
+def test_diagonal_pairs_switch(monkeypatch, shape):
+    """MUON_POLAR_DIAG_PAIRS=0: every upper tile a unit of its own again."""
+    monkeypatch.setenv("MUON_POLAR_DIAG_PAIRS", "0")
+    batch, m, n = shape
+    nt = -(-min(m, n) // 64)
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(2, 2, 2))
+    check(plan)
+    for s in (0, 1):
+        assert plan.stage[s].diag_pairs == 0
+        assert plan.stage[s].total_tiles == batch * nt * (nt + 1) // 2
+
+
+@pytest.mark.parametrize("shape", [(4, 512, 4096), (16, 256, 1024), (3, 1024, 4096)])
+def test_no_diagonal_pairs_where_rounds_stay_the_same(shape):
+    """Shapes whose units would take as many rounds as their tiles keep every tile."""
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(2, 2, 2))
+    check(plan)
+    assert plan.stage[0].diag_pairs == 0 and plan.stage[1].diag_pairs == 0
