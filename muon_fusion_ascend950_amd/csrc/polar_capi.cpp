@@ -309,8 +309,18 @@ int check_shape(int64_t batch, int64_t m, int64_t n) {
 // adds about a third to its throughput, so such a round is as good as full and
 // a split only adds fixups ([8,512,2048] gram: 288 tiles of 64x64 on 256 CUs,
 // unsplit 14.4 us against 18.9 us in 512 units; [3,1024,4096] 88 -> 82 us and
-// [8,1024,4096] 185 -> 176 us per step).
-int64_t sk_min_share(int bm, int bn) { return int64_t(bm) * bn >= 256 * 256 ? 20 : 8; }
+// [8,1024,4096] 185 -> 176 us per step).  And off when the units would outnumber
+// the CUs (two on some CUs, for the same reason): gram of 64x64 tiles at
+// [1,1024,4096] unsplit 37.7 against 43.2 us per step in 408 units, [2,768,3072]
+// 35.9 against 44.1, [4,512,4096] 35.5 against 39.8; with one unit per CU the
+// split still wins ([1,512,8192] 35.0 against 42.9, [1,700,5000] 43.2 against 49.5,
+// [2,512,4096] 30.6 against 32.5).  64x64 tiles (16 KiB partials, 0.2 us K-steps)
+// need shares of 16 K-steps: [2,150,2050] unsplit 25.6 against 27.7 us with
+// shares of 12.
+int64_t sk_min_share(int bm, int bn) {
+    const int64_t area = int64_t(bm) * bn;
+    return area >= 256 * 256 ? 20 : (area <= 64 * 64 ? 16 : 8);
+}
 
 SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident, int64_t cus,
                   int64_t min_share) {
@@ -319,7 +329,7 @@ SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident
     const int64_t rem = tiles % resident;
     if (rem == 0 || rem * 4 > resident * 3 || rem * 4 > cus * 3) return c;
     const int64_t units = std::min<int64_t>(resident, rem * 3) / 8 * 8;
-    if (units * 2 < rem * 3 || units < 8) return c;
+    if (units * 2 < rem * 3 || units < 8 || units > cus) return c;
     const int64_t iters = rem * k_steps;
     if (iters < min_share * units || iters >= (int64_t(1) << 31)) return c;
     c.dp_tiles = tiles - rem;
