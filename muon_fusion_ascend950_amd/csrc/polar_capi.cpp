@@ -168,7 +168,12 @@ std::unordered_map<PlanKey, Plan, PlanKeyHash> g_plans;
 // and otherwise 128x128 tiles (two workgroups per CU) when the batch has at
 // least half a tile per CU of them, else 64x64 ([1, 1024, 4096]: 64x64 gram and
 // poly tiles and 128x128 apply tiles take the step from 89.8 to 54.8 us; at
-// m = 2048, 128x128 is 2x faster than 256x256).  Stage 3 takes the largest of
+// m = 2048, 128x128 is 2x faster than 256x256).  Below a whole tile per CU of
+// 128x128, 64x64 tiles win while they are about one round of two per CU (at
+// most 2.25 per CU): [1,2048,4096] 98.6 -> 86.7 us, [4,1024,4096] 89.1 -> 80.8 us,
+// [1,2048,8192] 141.7 -> 133.9 us, [16,512,512] 30.8 -> 28.9 us; beyond, 128x128
+// stays faster ([2,1536,4096] 99.4 against 102.7 us, [1,2560,4096] 132.1 against
+// 156.3 us, [6,1024,2048] 68.9 against 74.8 us).  Stage 3 takes the largest of
 // 256x256 and 128x128 that gives every CU a tile, else 64x64.
 constexpr uint32_t kDefaultWaves = 8;
 
@@ -177,7 +182,12 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 uint32_t default_sym_tile(int64_t batch, int64_t s, int64_t large_from, int cus) {
     if (s >= large_from) return 256;
     const int64_t t = ceil_div(s, 128);
-    if (batch * (t * (t + 1) / 2) * 2 >= cus) return 128;
+    const int64_t tiles128 = batch * (t * (t + 1) / 2);
+    if (tiles128 >= cus) return 128;
+    if (2 * tiles128 >= cus) {
+        const int64_t t64 = ceil_div(s, 64);
+        return 4 * batch * (t64 * (t64 + 1) / 2) <= 9 * int64_t(cus) ? 64 : 128;
+    }
     return 64;
 }
 // The symmetric stages' tile where 256x256 tiles would leave most CUs idle (a

@@ -33,7 +33,7 @@ EXACT_COEFFS = (2.0, -1.0, 1.0)
 # shape splits no stage by default: gram and poly run one round of 192x192 tiles and
 # apply's last round runs as 256x128 halves, test_halves_gpu.py; it is split here
 # with 256x256 triangular tiles, and with the halves off.)
-SPLIT_SHAPES = [(2, 512, 4096), (1, 2000, 4040), (1, 700, 5000), (1, 2048, 8192)]
+SPLIT_SHAPES = [(2, 512, 4096), (2, 1536, 4096), (1, 700, 5000), (2, 1500, 3000)]
 # 256x256 tiles for the triangular stages (256 KiB partials)
 BIG_TILES = {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_POLY_TILE": "256"}
 # every stage of the headline split: 256x256 triangular tiles, apply's halves off
@@ -129,7 +129,7 @@ def test_split_agrees_with_unsplit_and_is_deterministic(monkeypatch, shape):
 
 
 def test_split_matches_oracle():
-    shape = (1, 2000, 4040)
+    shape = (2, 1500, 3000)
     x_cpu = O.make_input(shape, seed=23)
     y = polar_step(x_cpu.to(DEV), *C0)
     torch.cuda.synchronize()
