@@ -477,6 +477,19 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
                 continue;  // no partials, no arrival words
             }
         }
+        // A partial last round that stream-K leaves whole (its shares would be
+        // too short) runs as halves too, where they fit one round.
+        if (s == 2 && p.sk[s].sk_units == 0 && knobs.halves == 1 && sk_ok && occ > 0 &&
+            tiles_bm[s] == 256 && tiles_bn[s] == 256 && p.waves[s] == 8 && p.depth[s] == 2) {
+            const int64_t resident = int64_t(cus) * occ;
+            const int64_t rem = grids[s] % resident;
+            if (grids[s] > resident && rem > 0 && 4 * rem <= 3 * resident &&
+                4 * rem <= 3 * int64_t(cus) && (2 * rem) % 8 == 0 && 2 * rem <= resident) {
+                p.sk[s] = SkSplit{grids[s] - rem, static_cast<int32_t>(2 * rem), 0,
+                                  static_cast<int32_t>(knobs.halves_depth)};
+                continue;
+            }
+        }
         if (p.sk[s].sk_units > 0) {
             p.sk_any = true;
             const int64_t sk_tiles = grids[s] - p.sk[s].dp_tiles;

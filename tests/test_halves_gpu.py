@@ -5,7 +5,9 @@ resident workgroups, each of those tiles runs as two 256x128 column halves, one 
 workgroup, each over the whole K range, with the wave-pair kernel (two interleaved K
 chains per output): no fp32 partials, no arrival words, no fix-up.  At [4096,14336]
 (and the right-Gram form at [14336,4096]) that is 768 whole tiles and 256 halves.
-The checks:
+A short last round that stream-K leaves whole (its shares would be under 20 K-steps)
+runs as halves too: [2,2048,4352] 256 whole tiles and 32 halves, [1,3000,6000] 256 and
+64 (edge tiles: the last column tile's second half lies past n).  The checks:
 
 * the plan uses the halves at the headline shapes and leaves the workspace without
   apply partials;
@@ -57,10 +59,13 @@ def _cus() -> int:
     return torch.cuda.get_device_properties(0).multi_processor_count
 
 
-@pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)])
+SHORT_ROUNDS = [(2, 2048, 4352), (1, 3000, 6000), (2, 4352, 2048), (1, 6000, 3000)]
+
+
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)] + SHORT_ROUNDS)
 def test_headline_runs_halves(shape):
     capi = _capi()
-    plan = capi.check_plan(*shape, cus=_cus(), blocks_per_cu=(1, 1, 1))
+    plan = capi.check_plan(*shape, cus=_cus(), blocks_per_cu=(-1, -1, -1))
     apply = plan.stage[2]
     print(f"{shape}: apply dp {apply.dp_tiles} of {apply.total_tiles}, units {apply.sk_units}",
           flush=True)
@@ -69,7 +74,7 @@ def test_headline_runs_halves(shape):
     assert apply.partial_hi == 0 and apply.counter_hi == 0
 
 
-@pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)])
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)] + SHORT_ROUNDS)
 def test_exact_sums_are_bitwise(shape):
     capi = _capi()
     batch, m, n = shape
@@ -91,7 +96,7 @@ def test_exact_sums_are_bitwise(shape):
         assert_bits_equal(bits(y[i]), want, "Y")
 
 
-@pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)])
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)] + SHORT_ROUNDS)
 def test_halves_agree_with_split_and_unsplit(monkeypatch, shape):
     x = O.make_input(shape, seed=43).to(DEV)
     halves = polar_step(x, *C0)
@@ -107,18 +112,19 @@ def test_halves_agree_with_split_and_unsplit(monkeypatch, shape):
     assert_close_kernels(halves, unsplit)
 
 
-def test_halves_match_oracle():
-    x_cpu = O.make_input((1, 4096, 14336), seed=44)
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 3000, 6000), (1, 6000, 3000)])
+def test_halves_match_oracle(shape):
+    x_cpu = O.make_input(shape, seed=44)
     y = polar_step(x_cpu.to(DEV), *C0)
     torch.cuda.synchronize()
     assert_matches_oracle(y, x_cpu, [C0], rel_exact=1e-2)
 
 
-def test_halves_store_only_their_outputs():
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 3000, 6000)])
+def test_halves_store_only_their_outputs(shape):
     """Every element of Y is written (NaN fill replaced everywhere), and equal to the
     torch op's result."""
     capi = _capi()
-    shape = (1, 4096, 14336)
     x = O.make_input(shape, seed=45).to(DEV)
     y = torch.full_like(x, float("nan"))
     ws, _ = capi.alloc_workspace(*shape)

@@ -214,3 +214,16 @@ def test_no_diagonal_pairs_where_rounds_stay_the_same(shape):
     plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(2, 2, 2))
     check(plan)
     assert plan.stage[0].diag_pairs == 0 and plan.stage[1].diag_pairs == 0
+
+
+@pytest.mark.parametrize("shape", [(2, 2048, 4352), (1, 3000, 6000), (2, 4352, 2048),
+                                   (1, 6000, 3000), (1, 2560, 7000)])
+def test_short_last_round_runs_as_halves(shape):
+    """Apply's 256x256 tiles with a last round stream-K leaves whole (shares under 20
+    K-steps): that round runs as 256x128 halves, no partials, every tile covered."""
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(2, 2, 1))
+    check(plan)
+    e = plan.stage[2]
+    assert e.halves == 1 and (e.tile_m, e.tile_n, e.waves) == (256, 256, 8)
+    assert e.dp_tiles == e.total_tiles - e.total_tiles % 256
+    assert e.sk_units == 2 * (e.total_tiles % 256) > 0
