@@ -253,6 +253,18 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     // us (253 unsplit tiles against 136 tiles of 256x256 cut by stream-K; 4-wave
     // 192x192 tiles: 237.1 us).  Both forms (X rows or X columns as its K).
     uint32_t gram_tile = default_sym_tile(batch, s, 3072, cus);
+    // A long K (80 K-steps or more) pays for 256x256 gram tiles from s = 1536 when
+    // they number a quarter of the CUs or more: [6,1800,6000] 470.5 -> 450.1 us,
+    // [4,5248,2176] 372.4 -> 357.6 us, [3,2560,8192] 537.0 -> 508.4 us,
+    // [2,2048,8192] 245.4 -> 234.9 us, [1,3000,6000] 253.0 -> 239.4 us; with fewer
+    // tiles ([1,2048,8192]: 36) 128x128 and 64x64 stay 15-25% faster, as at 64
+    // K-steps ([16,1024,4096], [8,1600,4096]).
+    {
+        const int64_t t256 = ceil_div(s, 256);
+        if (gram_tile != 256 && s >= 1536 && ceil_div(std::max(m, n), 64) >= 80 &&
+            4 * batch * (t256 * (t256 + 1) / 2) >= cus)
+            gram_tile = 256;
+    }
     if (gram_tile == 256 && k.waves == 8 && k.pair == 1 && one_round_of_192(batch, s, cus))
         gram_tile = 192;
     k.gram_tile = static_cast<uint32_t>(env_u64("MUON_POLAR_GRAM_TILE", gram_tile));
