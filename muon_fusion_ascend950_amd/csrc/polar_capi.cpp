@@ -201,8 +201,14 @@ bool one_round_of_192(int64_t batch, int64_t s, int cus) {
     return cus > 0 && batch * (t256 * (t256 + 1) / 2) < cus && tiles <= cus && 4 * tiles > 3 * cus;
 }
 uint32_t default_apply_tile(int64_t batch, int64_t m, int64_t n, int cus) {
-    for (int64_t t : {256, 128})
-        if (batch * ceil_div(m, t) * ceil_div(n, t) >= cus) return static_cast<uint32_t>(t);
+    // 256x256 from three quarters of a round when K (min(m, n)) is 1024 or more:
+    // [1,3840,3840] (225 tiles) 245.6 -> 223.5 us per step against 128x128 tiles,
+    // [1,5248,2904] (252) 218.4 -> 202.5, [2,1792,3584] (196) 115.4 -> 105.6,
+    // [3,1024,4608] (216) 80.8 -> 75.9; [4,768,4096] (192, 12 K-steps) 61.7
+    // against 63.3 us keeps 128x128
+    const int64_t t256 = batch * ceil_div(m, 256) * ceil_div(n, 256);
+    if (t256 >= cus || (4 * t256 >= 3 * int64_t(cus) && std::min(m, n) >= 1024)) return 256;
+    if (batch * ceil_div(m, 128) * ceil_div(n, 128) >= cus) return 128;
     return 64;
 }
 
