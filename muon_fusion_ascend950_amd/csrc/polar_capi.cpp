@@ -272,6 +272,13 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
         if (gram_tile != 256 && s >= 1536 && ceil_div(std::max(m, n), 64) >= 80 &&
             4 * batch * (t256 * (t256 + 1) / 2) >= cus)
             gram_tile = 256;
+        // 64x64 gram tiles that outnumber the CUs (even as diagonal pairs) leave
+        // two long tiles on some CUs at 128 K-steps or more, where 128x128 tiles cut
+        // by stream-K share K evenly: [1,12352,1536] 183.6 -> 154.8 us per step
+        const int64_t t64 = ceil_div(s, 64);
+        if (gram_tile == 64 && ceil_div(std::max(m, n), 64) >= 128 &&
+            batch * (t64 * (t64 - 1) / 2 + (t64 + 1) / 2) > cus)
+            gram_tile = 128;
     }
     if (gram_tile == 256 && k.waves == 8 && k.pair == 1 && one_round_of_192(batch, s, cus))
         gram_tile = 192;
