@@ -261,7 +261,7 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     // us (253 unsplit tiles against 136 tiles of 256x256 cut by stream-K; 4-wave
     // 192x192 tiles: 237.1 us).  Both forms (X rows or X columns as its K).
     uint32_t gram_tile = default_sym_tile(batch, s, 3072, cus);
-    // A long K (80 K-steps or more) pays for 256x256 gram tiles from s = 1536 when
+    // A long K (80 K-steps or more) pays for 256x256 gram tiles from s = 1281 when
     // they number a quarter of the CUs or more: [6,1800,6000] 470.5 -> 450.1 us,
     // [4,5248,2176] 372.4 -> 357.6 us, [3,2560,8192] 537.0 -> 508.4 us,
     // [2,2048,8192] 245.4 -> 234.9 us, [1,3000,6000] 253.0 -> 239.4 us; with fewer
@@ -269,7 +269,7 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     // K-steps ([16,1024,4096], [8,1600,4096]).
     {
         const int64_t t256 = ceil_div(s, 256);
-        if (gram_tile != 256 && s >= 1536 && ceil_div(std::max(m, n), 64) >= 80 &&
+        if (gram_tile != 256 && s > 1280 && ceil_div(std::max(m, n), 64) >= 80 &&
             4 * batch * (t256 * (t256 + 1) / 2) >= cus)
             gram_tile = 256;
         // 64x64 gram tiles that outnumber the CUs (even as diagonal pairs) leave
