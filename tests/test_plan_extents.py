@@ -227,3 +227,27 @@ def test_short_last_round_runs_as_halves(shape):
     assert e.halves == 1 and (e.tile_m, e.tile_n, e.waves) == (256, 256, 8)
     assert e.dp_tiles == e.total_tiles - e.total_tiles % 256
     assert e.sk_units == 2 * (e.total_tiles % 256) > 0
+
+
+@pytest.mark.parametrize("shape", [(4, 1344, 6000), (4, 1496, 34240), (4, 1344, 20000)])
+def test_long_k_gram_takes_256_tiles_from_1281(shape):
+    """A gram of 80+ K-steps on A sides above 1280 takes 256x256 tiles cut by stream-K
+    when those tiles number a quarter of the CUs (4 x 21 = 84 here): every iteration
+    covered once, partial slots and arrival words inside the workspace."""
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(1, 1, 1))
+    check(plan)
+    e = plan.stage[0]
+    assert (e.tile_m, e.tile_n, e.waves) == (256, 256, 8)
+    assert e.k_steps >= 80 and e.total_tiles == 4 * 21 and e.sk_units > 0
+
+
+@pytest.mark.parametrize("shape", [(1, 1504, 10000), (1, 12352, 1536), (1, 10000, 1504)])
+def test_long_k_gram_takes_128_tiles_where_64_units_outnumber_the_cus(shape):
+    """A gram of 128+ K-steps whose 64x64 units (diagonal pairs counted) outnumber the
+    CUs (300 > 256 at A side 1504-1536) takes 128x128 tiles cut by stream-K, in the
+    wide form and in the right-Gram form (X columns as K)."""
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(1, 1, 1))
+    check(plan)
+    e = plan.stage[0]
+    assert (e.tile_m, e.tile_n) == (128, 128)
+    assert e.k_steps >= 128 and e.dp_tiles == 0 and e.sk_units > e.total_tiles

@@ -646,6 +646,18 @@ def test_beyond_baseline_shapes(shape):
     assert rel <= 1e-2, rel
 
 
+@pytest.mark.parametrize("shape", [(4, 1344, 5200), (1, 1504, 10000), (1, 12352, 1536)])
+def test_long_k_gram_tile_rules(shape):
+    """Shapes whose gram takes the long-K tile rules (256x256 tiles from A side 1281
+    with 80+ K-steps; 128x128 tiles where 64x64 units outnumber the CUs at 128+
+    K-steps, wide and right-Gram forms), both cut by stream-K: against the oracle's
+    float64 step and its rounding-point emulation, element by element."""
+    print(f"long-K gram rule {shape}", flush=True)
+    x = O.make_input(shape, seed=7)
+    y = run_steps(x, [C0])
+    assert_matches_oracle(y, x, [C0], rel_exact=1e-2)
+
+
 def test_svd_property_at_size():
     """One step maps singular values σ -> aσ + bσ³ + cσ⁵ (size-independent check)."""
     gen = torch.Generator().manual_seed(1)
