@@ -430,6 +430,9 @@ def main() -> int:
     ap.add_argument("--profile-muon", action="store_true",
                     help="only a loop of Muon updates of one fp32 [4096,14336] parameter, "
                          "for rocprofv3 runs")
+    ap.add_argument("--profile-shape", default=None, metavar="BxMxN",
+                    help="only --settle-s seconds, then W + K polar_step calls on one bf16 "
+                         "[B,M,N] input (e.g. 4x4096x4096), for rocprofv3 runs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -451,6 +454,18 @@ def main() -> int:
                                                 weight_decay=MUON_WD), args.steps, args.warmup)
         print(json.dumps({"profile": "muon_update fp32 [4096,14336]", "steps": args.steps,
                           "us_per_update": round(sec * 1e6, 2)}), flush=True)
+        return 0
+    if args.profile_shape:
+        shape = tuple(int(v) for v in args.profile_shape.split("x"))
+        xs = make_input(shape, seed=0).cuda()
+        fn = lambda: mf.polar_step(xs, a, b, c)  # noqa: E731
+        t_end = time.perf_counter() + args.settle_s
+        while time.perf_counter() < t_end:
+            fn()
+            torch.cuda.synchronize()
+        sec = time_calls(fn, args.steps, args.warmup)
+        print(json.dumps({"profile": "polar_step", "shape": list(shape), "steps": args.steps,
+                          "us_per_step": round(sec * 1e6, 2)}), flush=True)
         return 0
     if args.profile_configs:
         for name, shape, steps in CONFIGS:

@@ -67,12 +67,16 @@ struct Knobs {
     uint32_t halves_depth;  // LDS ring slots of those halves (2 or 3)
     uint32_t diag_pairs;    // 1: triangular stages pair their diagonal tiles where it
                             // takes fewer rounds of workgroups (below)
+    uint32_t sk_rounds;     // per stage (bit 0 gram, bit 1 poly, bit 2 apply): a stream-K
+                            // split of 256x256 tiles with a short last round also takes
+                            // the whole round before it (sk_policy)
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
                apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k &&
                waves == o.waves && depth[0] == o.depth[0] && depth[1] == o.depth[1] &&
                depth[2] == o.depth[2] && pair == o.pair && halves == o.halves &&
-               halves_depth == o.halves_depth && diag_pairs == o.diag_pairs;
+               halves_depth == o.halves_depth && diag_pairs == o.diag_pairs &&
+               sk_rounds == o.sk_rounds;
     }
 };
 
@@ -107,6 +111,7 @@ struct PlanKeyHash {
         mix(k.knobs.halves);
         mix(k.knobs.halves_depth);
         mix(k.knobs.diag_pairs);
+        mix(k.knobs.sk_rounds);
         return static_cast<size_t>(h);
     }
 };
@@ -254,6 +259,9 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     k.halves_depth = static_cast<uint32_t>(env_u64("MUON_POLAR_HALVES_DEPTH", 3));
     k.diag_pairs = static_cast<uint32_t>(env_u64("MUON_POLAR_DIAG_PAIRS", 1));
     if (k.diag_pairs > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_DIAG_PAIRS must be 0 or 1");
+    k.sk_rounds = static_cast<uint32_t>(env_u64("MUON_POLAR_SK_ROUNDS", 3));
+    if (k.sk_rounds > 7)
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_SK_ROUNDS must be a stage mask (0-7)");
     if (k.halves_depth != 2 && k.halves_depth != 3)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_HALVES_DEPTH must be 2 or 3");
     // Gram takes 192x192 tiles where poly does (one round of them fills the CUs,
@@ -360,7 +368,7 @@ int64_t sk_min_share(int bm, int bn) {
 }
 
 SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident, int64_t cus,
-                  int64_t min_share) {
+                  int64_t min_share, bool extra_round) {
     SkSplit c{tiles, 0, 0, 0};
     if (!enabled || resident < 8) return c;
     const int64_t rem = tiles % resident;
@@ -372,6 +380,24 @@ SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident
     c.dp_tiles = tiles - rem;
     c.sk_units = static_cast<int32_t>(units);
     c.sk_iters = iters;
+    // extra_round: where the last round is short enough to be cut in three pieces
+    // per tile, the split covers it and the whole round before it, one unit per
+    // resident workgroup (at most one per CU), each 1 + rem / resident tiles of
+    // K-steps: one round of whole tiles and a short cut round become one longer
+    // round whose tiles are mostly cut in two (one partial read in a fix-up instead
+    // of two), and the stage ends earlier.  Measured on MI355X with 256x256 gram
+    // and poly tiles (interleaved A/B, per step): [2,4096,8192] 862 -> 836 us,
+    // [8,4096,4096] 2035 -> 1993, [1,8192,16384] 3181 -> 3136, [4,4096,4096] 994
+    // -> 983, [1,6144,6144] 836 -> 829; a longer last round gains nothing
+    // ([3,4096,4096]: 152 of 256 tiles, 745 against 751 us), nor do 64x64 and
+    // 128x128 tiles (within 0.5%), nor apply ([4096,14336]: its column halves
+    // stay faster).
+    if (extra_round && rem * 3 <= resident && tiles >= rem + resident && resident <= cus &&
+        resident % 8 == 0 && (rem + resident) * k_steps < (int64_t(1) << 31)) {
+        c.dp_tiles = tiles - rem - resident;
+        c.sk_units = static_cast<int32_t>(resident);
+        c.sk_iters = (rem + resident) * k_steps;
+    }
     return c;
 }
 
@@ -480,7 +506,9 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
                       : muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s], tiles_bn[s],
                                                          p.waves[s], p.depth[s]);
         p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ, cus,
-                            sk_min_share(tiles_bm[s], tiles_bn[s]));
+                            sk_min_share(tiles_bm[s], tiles_bn[s]),
+                            (knobs.sk_rounds >> s & 1u) != 0 &&
+                                tiles_bm[s] * tiles_bn[s] >= 256 * 256);
         // Apply's cut round as 256x128 column halves, one per workgroup, where the
         // halves number between a half and a whole round of resident workgroups
         // (each half is then as long as a stream-K share, or shorter): the same

@@ -251,3 +251,42 @@ def test_long_k_gram_takes_128_tiles_where_64_units_outnumber_the_cus(shape):
     e = plan.stage[0]
     assert (e.tile_m, e.tile_n) == (128, 128)
     assert e.k_steps >= 128 and e.dp_tiles == 0 and e.sk_units > e.total_tiles
+
+
+@pytest.mark.parametrize("shape,rem", [((4, 4096, 4096), 32), ((2, 4096, 8192), 16),
+                                       ((1, 8192, 16384), 16), ((8, 4096, 4096), 64)])
+def test_short_last_round_splits_with_the_round_before(shape, rem):
+    """256x256 gram and poly tiles whose last round is at most a third of the CUs: the
+    split covers that round and the whole round before it, one unit per CU (most cut
+    tiles then have two contributors); MUON_POLAR_SK_ROUNDS=0 keeps the one-round split
+    of three pieces per tile."""
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(1, 1, 1))
+    check(plan)
+    for s in (0, 1):
+        e = plan.stage[s]
+        assert (e.tile_m, e.tile_n) == (256, 256)
+        assert e.total_tiles % 256 == rem
+        assert e.dp_tiles == e.total_tiles - rem - 256 and e.sk_units == 256
+
+
+def test_one_round_split_without_the_extra_round(monkeypatch):
+    monkeypatch.setenv("MUON_POLAR_SK_ROUNDS", "0")
+    plan = capi.check_plan(4, 4096, 4096, cus=256, blocks_per_cu=(1, 1, 1))
+    check(plan)
+    for s in (0, 1):
+        e = plan.stage[s]
+        assert e.dp_tiles == 512 and e.sk_units == 96
+
+
+def test_long_last_round_keeps_the_one_round_split():
+    """[3,4096,4096]: 152 tiles in the last round (over a third of the CUs)."""
+    plan = capi.check_plan(3, 4096, 4096, cus=256, blocks_per_cu=(1, 1, 1))
+    check(plan)
+    for s in (0, 1):
+        assert plan.stage[s].dp_tiles == 256 and plan.stage[s].sk_units == 256
+
+
+def test_sk_rounds_rejects_a_bad_mask(monkeypatch):
+    monkeypatch.setenv("MUON_POLAR_SK_ROUNDS", "8")
+    with pytest.raises(capi.CapiError):
+        capi.check_plan(4, 4096, 4096, cus=256)
