@@ -259,7 +259,7 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     k.halves_depth = static_cast<uint32_t>(env_u64("MUON_POLAR_HALVES_DEPTH", 3));
     k.diag_pairs = static_cast<uint32_t>(env_u64("MUON_POLAR_DIAG_PAIRS", 1));
     if (k.diag_pairs > 1) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_DIAG_PAIRS must be 0 or 1");
-    k.sk_rounds = static_cast<uint32_t>(env_u64("MUON_POLAR_SK_ROUNDS", 3));
+    k.sk_rounds = static_cast<uint32_t>(env_u64("MUON_POLAR_SK_ROUNDS", 7));
     if (k.sk_rounds > 7)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_SK_ROUNDS must be a stage mask (0-7)");
     if (k.halves_depth != 2 && k.halves_depth != 3)
@@ -390,8 +390,10 @@ SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident
     // [8,4096,4096] 2035 -> 1993, [1,8192,16384] 3181 -> 3136, [4,4096,4096] 994
     // -> 983, [1,6144,6144] 836 -> 829; a longer last round gains nothing
     // ([3,4096,4096]: 152 of 256 tiles, 745 against 751 us), nor do 64x64 and
-    // 128x128 tiles (within 0.5%), nor apply ([4096,14336]: its column halves
-    // stay faster).
+    // 128x128 tiles (within 0.5%).  Apply takes it only where its column halves
+    // (below) do not take the cut round ([4096,14336]: the halves stay, 671 against
+    // 677 us with this split instead): [1,5120,13312] 991 -> 972 us, [1,4096,17408]
+    // 798 -> 790, [1,6144,6144] 806.8 against 806.0.
     if (extra_round && rem * 3 <= resident && tiles >= rem + resident && resident <= cus &&
         resident % 8 == 0 && (rem + resident) * k_steps < (int64_t(1) << 31)) {
         c.dp_tiles = tiles - rem - resident;
@@ -507,7 +509,7 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
                                                          p.waves[s], p.depth[s]);
         p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ, cus,
                             sk_min_share(tiles_bm[s], tiles_bn[s]),
-                            (knobs.sk_rounds >> s & 1u) != 0 &&
+                            s < 2 && (knobs.sk_rounds >> s & 1u) != 0 &&
                                 tiles_bm[s] * tiles_bn[s] >= 256 * 256);
         // Apply's cut round as 256x128 column halves, one per workgroup, where the
         // halves number between a half and a whole round of resident workgroups
@@ -532,6 +534,12 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
                 continue;  // no partials, no arrival words
             }
         }
+        // Apply's two-round split (MUON_POLAR_SK_ROUNDS bit 2, sk_policy) where the
+        // halves above do not take its cut round.
+        if (s == 2 && p.sk[s].sk_units > 0 && (knobs.sk_rounds >> 2 & 1u) != 0 &&
+            tiles_bm[s] * tiles_bn[s] >= 256 * 256)
+            p.sk[s] = sk_policy(true, grids[s], ksteps[s], int64_t(cus) * occ, cus,
+                                sk_min_share(tiles_bm[s], tiles_bn[s]), true);
         // A partial last round that stream-K leaves whole (its shares would be
         // too short) runs as halves too, where they fit one round.
         if (s == 2 && p.sk[s].sk_units == 0 && knobs.halves == 1 && sk_ok && occ > 0 &&

@@ -290,3 +290,15 @@ def test_sk_rounds_rejects_a_bad_mask(monkeypatch):
     monkeypatch.setenv("MUON_POLAR_SK_ROUNDS", "8")
     with pytest.raises(capi.CapiError):
         capi.check_plan(4, 4096, 4096, cus=256)
+
+
+@pytest.mark.parametrize("shape,rem", [((1, 5120, 13312), 16), ((1, 4096, 17408), 64)])
+def test_apply_short_last_round_splits_with_the_round_before(shape, rem):
+    """Apply's 256x256 tiles with a short last round that the column halves do not
+    take (at most a quarter of the CUs as halves): the two-round split."""
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(1, 1, 1))
+    check(plan)
+    e = plan.stage[2]
+    assert e.halves == 0 and (e.tile_m, e.tile_n) == (256, 256)
+    assert e.total_tiles % 256 == rem
+    assert e.dp_tiles == e.total_tiles - rem - 256 and e.sk_units == 256
