@@ -111,9 +111,12 @@ int muon_polar_step(const void *x, void *y, void *workspace, size_t workspace_by
  * harnesses that forbid hipMalloc).  No reference counterpart.
  * The workspace is a device array of 192 MiB (201326592 bytes) inside the
  * library, one per GPU, held from the first call on that GPU until the process
- * ends; shapes whose workspace (info.workspace_bytes) is larger are rejected
- * with MUON_POLAR_ERR_WORKSPACE (e.g. [4, 4096, 4096]; [4096, 14336] fits).
- * Results equal muon_polar_step's bit for bit.  No device memory is allocated
+ * ends.  Where the step's plan needs a larger workspace (info.workspace_bytes)
+ * only for the partial slots of its two-round stream-K split, the plan without
+ * that split runs (MUON_POLAR_SK_ROUNDS=0, e.g. [2, 4096, 4096]); shapes that do
+ * not fit even so are rejected with MUON_POLAR_ERR_WORKSPACE (e.g.
+ * [4, 4096, 4096]; [4096, 14336] fits).  Results equal muon_polar_step's bit for
+ * bit under the same plan.  No device memory is allocated
  * and no caller buffer is needed beyond x and y.  Calls that overlap on one GPU
  * (other streams, other threads) share the array and race: serialise them. */
 int muon_polar_step_noalloc(const void *x, void *y, int64_t batch, int64_t m, int64_t n,

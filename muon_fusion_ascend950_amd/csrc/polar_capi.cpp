@@ -579,7 +579,9 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
     return MUON_POLAR_OK;
 }
 
-int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
+// one_round: the plan without the two-round stream-K split (MUON_POLAR_SK_ROUNDS
+// = 0), whose partial area is smaller (the allocation-free step falls back to it).
+int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out, bool one_round = false) {
     int st = check_shape(batch, m, n);
     if (st != MUON_POLAR_OK) return st;
     int device = 0;
@@ -588,6 +590,7 @@ int get_plan(int64_t batch, int64_t m, int64_t n, Plan &out) {
     Knobs knobs{};
     st = read_knobs(batch, m, n, cus > 0 ? cus : 256, knobs);
     if (st != MUON_POLAR_OK) return st;
+    if (one_round) knobs.sk_rounds = 0;
     const PlanKey key{device, batch, m, n, knobs};
     std::lock_guard<std::mutex> lock(g_plan_mutex);
     const auto found = g_plans.find(key);
@@ -1352,6 +1355,12 @@ int muon_polar_step_noalloc(const void *x, void *y, int64_t batch, int64_t m, in
     Plan p{};
     int st = get_plan(batch, m, n, p);
     if (st != MUON_POLAR_OK) return st;
+    // The two-round stream-K split's partial slots can outgrow the scratch where
+    // the one-round split fits ([2,4096,4096]: 259 against 143 MiB).
+    if (p.workspace_bytes > muon_polar::kNoAllocScratchBytes) {
+        st = get_plan(batch, m, n, p, true);
+        if (st != MUON_POLAR_OK) return st;
+    }
     if (p.workspace_bytes > muon_polar::kNoAllocScratchBytes)
         return fail(MUON_POLAR_ERR_WORKSPACE,
                     "this shape needs " + std::to_string(p.workspace_bytes) +

@@ -61,6 +61,29 @@ def test_noalloc_right_gram_form(capi):
     assert torch.equal(y, with_workspace(capi, x, O.COEFFICIENTS[0]))
 
 
+def test_noalloc_falls_back_to_the_one_round_split(capi, monkeypatch):
+    """[2,4096,4096]: the default plan's two-round stream-K split needs more than the
+    192 MiB scratch (its partial slots), the one-round split fits: the allocation-free
+    step runs that plan, bit for bit the workspace entry with MUON_POLAR_SK_ROUNDS=0,
+    and to bf16 precision the default plan."""
+    from tests.test_polar_step_gpu import assert_close_kernels
+
+    shape = (2, 4096, 4096)
+    assert capi.query(*shape).workspace_bytes > 192 << 20
+    print(f"noalloc fallback {shape}", flush=True)
+    x = O.make_input(shape, seed=5).to(DEV)
+    coeffs = O.COEFFICIENTS[0]
+    y = torch.empty_like(x)
+    capi.step_noalloc(x, y, *coeffs)
+    default = with_workspace(capi, x, coeffs)
+    monkeypatch.setenv("MUON_POLAR_SK_ROUNDS", "0")
+    assert capi.query(*shape).workspace_bytes <= 192 << 20
+    one_round = with_workspace(capi, x, coeffs)
+    torch.cuda.synchronize()
+    assert torch.equal(y, one_round)
+    assert_close_kernels(y, default)
+
+
 def test_noalloc_rejects_shapes_beyond_its_scratch(capi):
     info = capi.query(4, 4096, 4096)
     assert info.workspace_bytes > 192 << 20
