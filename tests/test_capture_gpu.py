@@ -44,10 +44,12 @@ def polar_step(x, a, b, c):
     return ps(x, a, b, c)
 
 
-@pytest.mark.parametrize("shape", [(8, 512, 2048), (2, 768, 4096), (2, 150, 2050)])
+@pytest.mark.parametrize("shape", [(8, 512, 2048), (2, 768, 4096), (2, 150, 2050),
+                                   (2, 4096, 4096)])
 def test_graph_replays_match_eager(shape):
     """(2, 768, 4096) splits its gram stage (stream-K arrival words in the graph's
-    workspace); (2, 150, 2050) runs the register-staged kernels."""
+    workspace); (2, 150, 2050) runs the register-staged kernels; (2, 4096, 4096) splits
+    gram and poly over two rounds (units over two or three tiles each)."""
     x_static = O.make_input(shape, seed=30).to(DEV)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -68,7 +70,8 @@ def test_graph_replays_match_eager(shape):
         assert torch.equal(y_static, want), f"replay {r} differs from eager"
 
 
-@pytest.mark.parametrize("shape", [(1, 4096, 14336), (2, 1024, 4096), (8, 512, 2048)])
+@pytest.mark.parametrize("shape", [(1, 4096, 14336), (2, 1024, 4096), (8, 512, 2048),
+                                   (2, 4096, 4096)])
 def test_garbage_workspace_and_shared_workspace_replays(shape):
     """The C ABI step on a workspace filled with random bytes equals the step on a zeroed
     one, bit for bit; a graph that captured a step on one workspace still replays
