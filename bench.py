@@ -68,7 +68,8 @@ CONFIGS = (
     ("cfg4", (4, 4096, 4096), 1),
     ("cfg4", (4, 4096, 4096), 5),
 )
-# CPU baseline shapes: shape and runs after one warm-up
+# CPU baseline shapes (every BASELINE.json configuration's shape): shape and runs after
+# one warm-up
 CPU_SHAPES = (((129, 130), 50), ((2, 150, 2050), 50), ((8, 512, 2048), 50), ((4096, 14336), 40),
               ((4, 4096, 4096), 20))
 TRAFFIC_SUMMARY = ROOT / "profiles" / "apply_4096x14336_hbm_traffic.txt"
@@ -363,6 +364,11 @@ def cpu_baseline() -> dict:
                    f"({med * 1e3:.0f} ms/step); other BASELINE shapes in 'shapes'"),
         "torch_threads": torch.get_num_threads(),
         "affinity_cores": affinity,
+        "thread_policy": (f"min(affinity cores {affinity}, OMP_NUM_THREADS {share}): the GPU box's "
+                          f"host share is 16 threads per GPU; the baseline plan asks for every "
+                          f"affinity core"
+                          + (", which this equals" if cores == affinity else
+                             f", {affinity - cores} of which are left out by the cap")),
         **cpu_info(),
         "shapes": rows,
     }

@@ -106,7 +106,8 @@ hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const Ge
 bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth);
 
 // Waves per workgroup the DMA-fed kernel of a bm x bn tile runs with, given the
-// requested count (8 is available for 256x256 and 128x128 tiles; 4 otherwise).
+// requested count (8 is available for 256x256, 192x192 (the wave pairs) and
+// 128x128 tiles; 4 otherwise).
 int stream_waves(int bm, int bn, int requested);
 
 // Workgroups of the DMA-fed kernel for (s, bm, bn, waves, depth) resident per CU

@@ -1059,9 +1059,11 @@ __global__ __launch_bounds__(512) void polar_stream_halves_kernel(GemmArgs g) {
 // Instantiated (tile, waves, depth) combinations: 256x256 with 8 or 4 waves and
 // two slots; 128x128 with 8 or 4 waves and 2 or 4 slots of 32 KiB (8 waves: two
 // per SIMD, 64x32 wave tiles; [16,512,2048] 62.5 -> 59.0 us, [1,1024,4096]
-// 46.3 -> 43.9 us against 4 waves); other tiles with 4 waves and the depths their
-// LDS allows (64x64: 2, 4 or 8 of 16 KiB; 128x256 and 256x128: 2 or 3 of 48 KiB;
-// 192x192: 2; a third 48 KiB slot measured no faster at [4096,14336]).
+// 46.3 -> 43.9 us against 4 waves); 192x192 with 8 waves (the wave pairs) and 2
+// or 3 slots of 48 KiB (three by default: [4096,14336] gram 225 -> 212 us, poly
+// 75 -> 72 us), or with 4 waves and 2 slots; other tiles with 4 waves and the
+// depths their LDS allows (64x64: 2, 4 or 8 of 16 KiB; 128x256 and 256x128: 2 or 3
+// of 48 KiB).
 template <int BM, int BN>
 constexpr bool depth_ok(int waves, int depth) {
     if (BM == 256 && BN == 256) return depth == 2 && (waves == 8 || waves == 4);

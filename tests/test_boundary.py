@@ -383,3 +383,18 @@ def test_in_place_step_and_apply_are_rejected():
     assert st == capi.ERR_INVALID_ARGUMENT and "must not overlap" in capi.last_error()
     st = lib.muon_polar_apply(ws, x, ws + 256, None, 0, 1, 64, 128, 1.0, None)
     assert st == capi.ERR_INVALID_ARGUMENT and "poly and y must not overlap" in capi.last_error()
+
+
+def test_noalloc_rejects_shapes_beyond_its_scratch_before_any_launch():
+    """muon_polar_step_noalloc's size check runs on the host before any device call:
+    [4,4096,4096] needs more than its 192 MiB scratch even with the one-round split
+    (A and P alone are 256 MiB), so it is rejected.  The non-null pointers are never
+    dereferenced."""
+    lib = capi.load()
+    info = capi.query(4, 4096, 4096)
+    assert 2 * info.gram_bytes > 192 << 20
+    st = lib.muon_polar_step_noalloc(16, 1 << 40, 4, 4096, 4096, 1.0, 1.0, 1.0, None)
+    assert st == capi.ERR_WORKSPACE
+    assert "muon_polar_step_noalloc holds" in capi.last_error()
+    # a null x or y is refused first
+    assert lib.muon_polar_step_noalloc(None, 16, 1, 8, 8, 1.0, 1.0, 1.0, None) == capi.ERR_INVALID_ARGUMENT

@@ -3,7 +3,7 @@
 
 * A captured step (three stage kernels, workspace from the graph's pool) replays
   bit-identically to eager calls, replay after replay, with eager work on the same buffers
-  in between (SURVEY.md §8(f) 4; the reference never tested capture).  The stream-K arrival
+  in between (the reference never tested capture).  The stream-K arrival
   words carry a launch token: a replay reuses its captured token and finds the zero counts
   its last run left, eager launches on the same workspace in between use other tokens.
 * A workspace full of garbage gives the same bits as a fresh one (no clearing needed).

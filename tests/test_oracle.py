@@ -317,3 +317,70 @@ def test_normalization_closed_forms():
     norm = O.bf16_round(np.sqrt((x * x).sum(axis=(-2, -1), keepdims=True)))
     wrong = O.bf16_round(x.astype(np.float32) / O.bf16_round(norm + np.float32(1e-6)))
     assert not np.array_equal(wrong, O.normalize_reference_rounding(x))
+
+
+# ----------------------------------------------------------------------------- ulp metric
+def _bf16_rank_table():
+    """Rank of every finite bf16 bit pattern among the distinct finite bf16 values
+    (+0 and -0 share one rank): an independent definition of ulp distance, from
+    torch's own bf16 -> fp32 conversion and a sort."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    vals = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).float().numpy()
+    finite = np.isfinite(vals)
+    distinct = np.unique(vals[finite])  # -0.0 == 0.0 collapse into one entry
+    rank = np.full(1 << 16, -1, dtype=np.int64)
+    rank[finite] = np.searchsorted(distinct, vals[finite])
+    return bits, finite, rank
+
+
+def test_bf16_ulp_distance_is_the_rank_distance_between_finite_values():
+    """The metric used by the GPU parity gates counts the bf16 values between two
+    patterns: checked against the rank of each value among all finite bf16 values,
+    on adjacent pairs over the whole range, on random pairs, across zero, and on
+    signed zeros."""
+    bits, finite, rank = _bf16_rank_table()
+    fb = bits[finite]
+    # adjacent patterns of the same sign: distance 1 (exponent boundaries included)
+    pos = fb[fb < 0x7F80]
+    pos = pos[pos > 0]
+    assert np.all(O.bf16_ulp_distance(pos[1:], pos[:-1]) == 1)
+    assert O.bf16_ulp_distance([0x3F7F], [0x3F80])[0] == 1  # 1 - 2^-8 .. 1.0
+    neg = np.sort(fb[(fb > 0x8000) & (fb < 0xFF80)])
+    assert np.all(O.bf16_ulp_distance(neg[1:], neg[:-1]) == 1)
+    # signed zeros are one value
+    assert O.bf16_ulp_distance([0x0000], [0x8000])[0] == 0
+    # across zero: the two distances to zero add up
+    assert O.bf16_ulp_distance([0x0001], [0x8001])[0] == 2
+    assert O.bf16_ulp_distance([0x3F80], [0xBF80])[0] == 2 * rank[0x3F80] - 2 * rank[0x0000]
+    # random pairs of finite patterns against the rank table
+    rng = np.random.default_rng(99)
+    a = rng.choice(fb, 20000)
+    b = rng.choice(fb, 20000)
+    np.testing.assert_array_equal(O.bf16_ulp_distance(a, b), np.abs(rank[a] - rank[b]))
+    # and a few large pairs, where the counts must not wrap
+    assert O.bf16_ulp_distance([0x7F7F], [0xFF7F])[0] == rank[0x7F7F] - rank[0xFF7F]
+
+
+def test_bf16_ulp_distance_rejects_planted_mistakes():
+    """Plausible wrong maps fail the checks above: no sign handling (raw bit
+    difference), and a sign map off by one (signed zeros one ulp apart)."""
+    bits, finite, rank = _bf16_rank_table()
+
+    def no_sign(a_bits, b_bits):
+        return np.abs(np.asarray(a_bits, dtype=np.int32) - np.asarray(b_bits, dtype=np.int32))
+
+    def off_by_one(a_bits, b_bits):
+        def ordered(v):
+            v = np.asarray(v, dtype=np.uint16).astype(np.int32)
+            return np.where(v & 0x8000, 0x7FFF - v, v)
+
+        return np.abs(ordered(a_bits) - ordered(b_bits))
+
+    assert no_sign([0x0001], [0x8001])[0] != 2
+    assert off_by_one([0x0000], [0x8000])[0] != 0
+    rng = np.random.default_rng(5)
+    fb = bits[finite]
+    a, b = rng.choice(fb, 1000), rng.choice(fb, 1000)
+    want = np.abs(rank[a] - rank[b])
+    assert not np.array_equal(no_sign(a, b), want)
+    assert not np.array_equal(off_by_one(a, b), want)
