@@ -249,6 +249,60 @@ def stage_times(batch: int, m: int, n: int, launches: int, repeats: int = 3) -> 
             "apply": per["apply"], "step": per["step"]}
 
 
+def instep_kernel_times(batch: int, m: int, n: int, steps: int) -> dict:
+    """µs of each stage kernel inside eager steps: `steps` steps run as their three stage
+    calls through the C ABI (polar_step's workspace, the step's own plan and split, so
+    each call is the kernel the step launches, in its place), with a HIP event recorded
+    on the launch stream before gram and after each stage; the median over the steps of
+    each interval.  Unlike stage_times (differences of graph replays) every kernel is
+    timed directly where it runs, its dispatch from the stream's queue included; each
+    timed event also adds a release between two kernels, so the intervals over-state
+    the kernels by that much ("step" against an untimed step shows it)."""
+    import torch
+    from muon_fusion_ascend950_amd import capi
+
+    x = make_input((batch, m, n), seed=0).cuda()
+    ws, info = capi.alloc_workspace(batch, m, n)
+    mp = info.padded_rows
+    p_off = -(-info.gram_bytes // 256) * 256
+    gram = ws[:info.gram_bytes].view(torch.bfloat16).view(batch, mp, mp)
+    poly = ws[p_off:p_off + info.gram_bytes].view(torch.bfloat16).view(batch, mp, mp)
+    y = torch.empty_like(x)
+    a, b, c = COEFFS
+    calls = (lambda: capi.gram(x, gram, workspace=ws),
+             lambda: capi.poly(gram, poly, batch, m, n, b, c, workspace=ws),
+             lambda: capi.apply(poly, x, y, a, workspace=ws))
+    for call in calls:
+        call()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for ev in events:
+        ev[0].record()
+        for i, call in enumerate(calls):
+            call()
+            ev[i + 1].record()
+    torch.cuda.synchronize()
+    per = {name: statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1e3 for ev in events)
+           for i, name in enumerate(STAGES)}
+    per["step"] = statistics.median(ev[0].elapsed_time(ev[3]) * 1e3 for ev in events)
+    return per
+
+
+def sustained(fn, seconds: float) -> tuple:
+    """µs per call over `seconds` of back-to-back calls (synchronised once a second)."""
+    import torch
+
+    calls = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(50):
+            fn()
+        calls += 50
+        torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / calls, calls
+
+
 # ----------------------------------------------------------------------------- comparison points
 MUON_LR, MUON_MOMENTUM, MUON_WD = 0.02, 0.95, 0.01
 
@@ -304,7 +358,13 @@ def run_metadata() -> dict:
                    "all_configs: 20 warm-ups, median of 5 x 100 calls (README.md:179-191); "
                    "kernel_us: HIP-graph replays of R steps, R (poly, apply) and R apply "
                    "between HIP events on the launch stream; stage times are their "
-                   "differences"),
+                   "differences (roofline.achieved uses apply); event_kernel_us: R eager "
+                   "steps as their three stage launches with a HIP event recorded after "
+                   "each, median interval per stage: every stage timed where it runs, but "
+                   "each timed event adds a release between kernels (event_step_us against "
+                   "graph_step_us shows its cost), so these over-state each kernel; "
+                   "sustained: back-to-back headline calls for sustained.seconds after "
+                   "the K timed calls"),
     }
 
 
@@ -410,7 +470,7 @@ def headline_phase(args, x):
     settled = settle(step, args.settle_s)
     sec = time_calls(step, args.steps, args.warmup)
     torch.cuda.synchronize()
-    return gate, settled, sec
+    return gate, settled, sec, step
 
 
 def main() -> int:
@@ -423,6 +483,9 @@ def main() -> int:
     ap.add_argument("--stage-launches", type=int, default=50,
                     help="repetitions of each stage sequence (step, tail, apply) in the "
                          "graph-replayed stage timing")
+    ap.add_argument("--sustain-s", type=float, default=2.0,
+                    help="seconds of back-to-back headline calls after the timed K (the "
+                         "'sustained' figure; 0 skips it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile", action="store_true",
                     help="only the headline phase (gate, settle, W + K steps), the stage "
@@ -495,16 +558,22 @@ def main() -> int:
 
     # ---- headline: [4096,14336], one step (the driver contract)
     x = make_input((m, n), seed=0).cuda()
-    gate, settled, sec = headline_phase(args, x)
+    gate, settled, sec, step_fn = headline_phase(args, x)
     flops = credited_flops(batch, m, n)
     tflops = flops / sec / 1e12
     print(json.dumps({"phase": "headline", "us_per_step": round(sec * 1e6, 2),
                       "settle_calls": settled, **gate}), file=sys.stderr, flush=True)
+    # 2 s of back-to-back headline calls: the rate a long optimizer run sustains
+    sec_sus, calls_sus = sustained(step_fn, args.sustain_s) if args.sustain_s > 0 else (None, 0)
     st = stage_times(batch, m, n, launches=args.stage_launches)
+    ist = instep_kernel_times(batch, m, n, steps=args.stage_launches)
     apply_flops = 2 * batch * m * m * n
+    # the roofline's duration: apply launches back to back in a replayed graph (no host
+    # gaps, no event between kernels; its rocprof trace agrees with the in-step one)
     achieved = apply_flops / (st["apply"] * 1e-6) / 1e12
     b2, m2, n2 = SECONDARY
     st2 = stage_times(b2, m2, n2, launches=max(args.stage_launches, 100))
+    ist2 = instep_kernel_times(b2, m2, n2, steps=max(args.stage_launches, 100))
     if args.profile:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -515,6 +584,7 @@ def main() -> int:
                           "warmup": args.warmup, "settle_calls": settled,
                           "us_per_step": round(sec * 1e6, 2),
                           "kernel_us": {k: round(st[k], 2) for k in STAGES},
+                          "event_kernel_us": {k: round(ist[k], 2) for k in STAGES},
                           "graph_step_us": round(st["step"], 2),
                           "secondary_kernel_us": {k: round(st2[k], 2) for k in STAGES},
                           "secondary_graph_step_us": round(st2["step"], 2),
@@ -580,14 +650,21 @@ def main() -> int:
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
         "accuracy": gate,
         "settle": {"seconds": args.settle_s, "calls": settled},
+        "sustained": ({"seconds": args.sustain_s, "calls": calls_sus,
+                       "us_per_step": round(sec_sus * 1e6, 2),
+                       "pct_bf16_peak": round(100 * flops / sec_sus / 1e12 / PEAK_BF16_TFLOPS, 2)}
+                      if sec_sus else None),
         "kernel_us": {k: round(st[k], 2) for k in STAGES},
         "kernel_us_sum": round(sum(st[k] for k in STAGES), 2),
         "graph_step_us": round(st["step"], 2),
+        "event_kernel_us": {k: round(ist[k], 2) for k in STAGES},
+        "event_step_us": round(ist["step"], 2),
         "torch_eager_us": round(eager * 1e6, 2),
         "speedup_vs_torch_eager": round(eager / sec, 3),
         "roofline": {
             "bound": "mfma",
-            "kernel": "stage 3 apply (Y = a·X + P·X), 481.0 GFLOP per launch",
+            "kernel": ("stage 3 apply (Y = a·X + P·X), 481.0 GFLOP per launch, over kernel_us.apply "
+                       "(graph-replayed apply launches between HIP events on the launch stream)"),
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
@@ -618,6 +695,7 @@ def main() -> int:
             "accuracy": gate2,
             "kernel_us": {k: round(st2[k], 2) for k in STAGES},
             "kernel_us_sum": round(sum(st2[k] for k in STAGES), 2),
+            "event_kernel_us": {k: round(ist2[k], 2) for k in STAGES},
             "graph_step_us": round(st2["step"], 2),
             "torch_eager_us": round(eager2 * 1e6, 2),
             "speedup_vs_torch_eager": round(eager2 / sec2, 3),

@@ -70,13 +70,16 @@ struct Knobs {
     uint32_t sk_rounds;     // per stage (bit 0 gram, bit 1 poly, bit 2 apply): a stream-K
                             // split of 256x256 tiles with a short last round also takes
                             // the whole round before it (sk_policy)
+    uint32_t y_cpol, ap_cpol;  // cache policy of the DMA-fed kernels' Y / A and P stores
+                               // (GemmArgs::out_cpol)
     bool operator==(const Knobs &o) const {
         return gram_tile == o.gram_tile && poly_tile == o.poly_tile && apply_bm == o.apply_bm &&
                apply_bn == o.apply_bn && stream == o.stream && stream_k == o.stream_k &&
                waves == o.waves && depth[0] == o.depth[0] && depth[1] == o.depth[1] &&
                depth[2] == o.depth[2] && pair == o.pair && halves == o.halves &&
                halves_depth == o.halves_depth && diag_pairs == o.diag_pairs &&
-               sk_rounds == o.sk_rounds;
+               sk_rounds == o.sk_rounds && y_cpol == o.y_cpol &&
+               ap_cpol == o.ap_cpol;
     }
 };
 
@@ -112,6 +115,7 @@ struct PlanKeyHash {
         mix(k.knobs.halves_depth);
         mix(k.knobs.diag_pairs);
         mix(k.knobs.sk_rounds);
+        mix(uint64_t(k.knobs.y_cpol) << 8 | k.knobs.ap_cpol);
         return static_cast<size_t>(h);
     }
 };
@@ -137,6 +141,7 @@ struct Plan {
     int64_t gram_grid, poly_grid, apply_grid;
     size_t gram_bytes, workspace_bytes;
     bool stream;
+    int y_cpol, ap_cpol;  // store cache policies (GemmArgs::out_cpol)
     int waves[3];  // waves per workgroup of the DMA-fed kernel of each stage
     int depth[3];  // LDS ring slots of the DMA-fed kernel of each stage
     // polar_step's stream-K splits (gram, poly, apply) and their workspace areas
@@ -262,6 +267,19 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     k.sk_rounds = static_cast<uint32_t>(env_u64("MUON_POLAR_SK_ROUNDS", 7));
     if (k.sk_rounds > 7)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_SK_ROUNDS must be a stage mask (0-7)");
+    // Cache policy of the output stores: device-scope (sc1) stores of A, P and Y
+    // leave no dirty lines in the XCD's L2 for the end-of-kernel write-back, and
+    // the next kernel (poly, apply, the next step's gram) reads them from the
+    // memory-side cache.  Interleaved A/B against the previous policy (Y
+    // non-temporal, A and P plain), all results bit-identical: five-step chains
+    // [8,512,2048] 37.7 -> 34.6 us per step, [1,1024,4096] 42.8 -> 38.7, [8,2048,512]
+    // 37.9 -> 34.3, [2,2048,8192] 249.9 -> 244.1; single steps [8,512,2048] 34.7 ->
+    // 34.2, [4096,14336] 671.7 -> 664.6 and 694.0 -> 690.9 (two boxes), [14336,4096]
+    // 678.6 -> 672.5; [4,4096,4096] unchanged.
+    k.y_cpol = static_cast<uint32_t>(env_u64("MUON_POLAR_Y_CPOL", 2));
+    k.ap_cpol = static_cast<uint32_t>(env_u64("MUON_POLAR_AP_CPOL", 2));
+    if (k.y_cpol > 4 || k.ap_cpol > 4)
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_Y_CPOL / _AP_CPOL must be 0..4");
     if (k.halves_depth != 2 && k.halves_depth != 3)
         return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_HALVES_DEPTH must be 2 or 3");
     // Gram takes 192x192 tiles where poly does (one round of them fills the CUs,
@@ -447,6 +465,8 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
     // The right-Gram stages exist only as DMA-fed kernels: MUON_POLAR_STREAM=0
     // selects the register-staged kernels for m <= n alone.
     p.stream = knobs.stream != 0 || tall;
+    p.y_cpol = static_cast<int>(knobs.y_cpol);
+    p.ap_cpol = static_cast<int>(knobs.ap_cpol);
     if (p.gram_grid >= (int64_t(1) << 31) || p.apply_grid >= (int64_t(1) << 31))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "grid too large");
 
@@ -738,6 +758,7 @@ StageLaunch gram_launch(const Plan &p, const void *x, int64_t ldx, void *gram, i
     L.stream_ok = p.stream && dma;
     L.vec = vec;
     L.grid = p.gram_grid;
+    g.out_cpol = p.ap_cpol;
     return L;
 }
 
@@ -767,6 +788,7 @@ StageLaunch poly_launch(const Plan &p, const void *gram, void *poly, double b, d
     L.stream_ok = p.stream;
     L.vec = true;
     L.grid = p.poly_grid;
+    g.out_cpol = p.ap_cpol;
     return L;
 }
 
@@ -800,6 +822,7 @@ StageLaunch apply_launch(const Plan &p, const void *poly, const void *x, int64_t
     L.extent[1] = L.extent[2] = m * ldx * 2;
     g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : 0;
     g.group_n = apply_group(p);
+    g.out_cpol = p.y_cpol;
     // DMA-fed kernel: X rows of whole 16-byte chunks (Y any alignment: 2-byte
     // stores when out_vec is 0); register-staged kernel: vectors on both or neither.
     const bool xvec = (ldx % 8 == 0) && aligned16(x);
@@ -846,6 +869,7 @@ StageLaunch gram_t_launch(const Plan &p, const void *x, int64_t ldx, void *gram,
     L.stream_ok = true;
     L.vec = true;
     L.grid = p.gram_grid;
+    g.out_cpol = p.ap_cpol;
     return L;
 }
 
@@ -879,6 +903,7 @@ StageLaunch apply_r_launch(const Plan &p, const void *poly, const void *x, int64
     L.extent[1] = p.mp * p.mp * 2;
     g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : 0;
     g.group_n = apply_group(p);
+    g.out_cpol = p.y_cpol;
     L.k_tail = ldx % 64 != 0;
     L.stage = Stage::ApplyR;
     L.sk_index = 2;

@@ -45,6 +45,8 @@ struct GemmArgs {
     int32_t out_rows, out_cols;              // store extent (apply only)
     int32_t out_vec;                         // 1: out rows take 16-byte stores; 0: 2-byte
                                              // stores (rows of n % 8 != 0 elements)
+    int32_t out_cpol;                        // DMA-fed kernels' output stores: 0 plain, 1 nt,
+                                             // 2 sc1, 3 nt sc1, 4 sc0 sc1
     int32_t tiles_m, tiles_n, tiles_per_batch;
     float s_epi, s_acc;  // poly: b, c;  apply: a, 1
     // streaming kernels only

@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_scale_kernel(const uint16_t
                 const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(v[w] >> 16) / d);
                 o[w] = lo | (hi << 16);
             }
-            *reinterpret_cast<u32x4 *>(yb + e) = o;
+            store16_sc1(yb + e, o);
         }
     } else {
         for (int64_t e = e0 + threadIdx.x; e < e1; e += kNormThreads)
@@ -173,9 +173,9 @@ __global__ __launch_bounds__(kNormThreads) void muon_momentum_kernel(
             if (kVec) {
                 *reinterpret_cast<f32x4 *>(buf + base + e) = f32x4{nb[0], nb[1], nb[2], nb[3]};
                 *reinterpret_cast<f32x4 *>(buf + base + e + 4) = f32x4{nb[4], nb[5], nb[6], nb[7]};
-                *reinterpret_cast<u32x4 *>(x0 + base + e) =
-                    u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                          h[6] | (h[7] << 16)};
+                store16_sc1(x0 + base + e,
+                            u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                  h[6] | (h[7] << 16)});
             } else {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(kNormThreads) void pad_rows_kernel(const uint16_t *
             v = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
                       h[6] | (h[7] << 16)};
         }
-        *reinterpret_cast<u32x4 *>(xp + q * 8) = v;
+        store16_sc1(xp + q * 8, v);
     }
 }
 

@@ -252,6 +252,13 @@ __device__ __forceinline__ void wait_vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
+// 16-byte store at device scope (sc1): written through the XCD's L2, so the line is
+// not dirty there when the kernel ends, and a kernel on another XCD reads the data
+// from the memory side.  For buffers the next kernel of a step reads.
+__device__ __forceinline__ void store16_sc1(void *p, u32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N <= 63, "vmcnt range");
