@@ -642,6 +642,17 @@ int finish_stage(hipError_t launch, hipStream_t stream, const char *stage) {
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+// Whether the DMA-fed kernels read X rows `ldx` elements apart in place: rows of
+// whole 16-byte chunks (16-byte aligned X), or rows of an even number of elements
+// starting on 4-byte boundaries, whose chunks the 16-byte DMA reads at 4-byte
+// aligned addresses (the chunk that straddles a row's end is masked: gram zeroes
+// its positions past n in LDS, apply only feeds it to output columns >= n, which
+// are not stored).
+bool dma_rows(int64_t ldx, const void *x) {
+    return ldx % 8 == 0 ? aligned16(x) : (ldx % 2 == 0 && aligned4(x));
+}
 
 // Whether byte ranges [a, a + a_bytes) and [b, b + b_bytes) share a byte.
 bool overlaps(const void *a, size_t a_bytes, const void *b, size_t b_bytes) {
@@ -718,8 +729,9 @@ struct StageLaunch {
     // GemmArgs fields are 32-bit)
     int64_t extent[3];
     // X rows read in place end inside the last K-step (ldx % 64 != 0): the
-    // kernel masks that step's chunks past row_k (gram and apply-right)
-    bool k_tail;
+    // kernel masks that step's chunks past row_k (gram and apply-right); 2: rows
+    // of ldx % 8 != 0 elements (gram), whose chunk straddling n is also masked
+    int k_tail;
     GemmArgs g;
 };
 
@@ -748,8 +760,8 @@ StageLaunch gram_launch(const Plan &p, const void *x, int64_t ldx, void *gram, i
     const bool vec = (ldx % 8 == 0) && aligned16(x);
     // DMA-fed: X rows are K-contiguous panels of 16-byte chunks; a last K-step
     // past n (ldx % 64 != 0) is loaded with its chunks past n masked
-    const bool dma = vec;
-    L.k_tail = ldx % 64 != 0;
+    const bool dma = dma_rows(ldx, x);
+    L.k_tail = ldx % 64 == 0 ? 0 : ldx % 8 == 0 ? 1 : 2;
     L.stage = Stage::Gram;
     L.sk_index = 0;
     L.bm = L.bn = p.gram_tile;
@@ -832,7 +844,7 @@ StageLaunch apply_launch(const Plan &p, const void *poly, const void *x, int64_t
     L.bn = p.apply_bn;
     L.waves = p.waves[2];
     L.depth = p.depth[2];
-    L.stream_ok = p.stream && xvec;
+    L.stream_ok = p.stream && dma_rows(ldx, x);
     L.vec = xvec && g.out_vec;
     L.grid = p.apply_grid;
     return L;
@@ -904,7 +916,7 @@ StageLaunch apply_r_launch(const Plan &p, const void *poly, const void *x, int64
     g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : 0;
     g.group_n = apply_group(p);
     g.out_cpol = p.y_cpol;
-    L.k_tail = ldx % 64 != 0;
+    L.k_tail = ldx % 64 != 0 ? 1 : 0;
     L.stage = Stage::ApplyR;
     L.sk_index = 2;
     L.bm = p.apply_bm;
@@ -1005,11 +1017,14 @@ int check_tall(const Plan &p, const void *x, const void *y) {
     return MUON_POLAR_OK;
 }
 
-// Rows of n % 8 != 0 elements: copy X into the workspace's zero-padded buffer
+// Rows of n % 8 != 0 elements that the DMA-fed kernels cannot read in place (an
+// odd n, or X not 4-byte aligned): copy X into the workspace's zero-padded buffer
 // and point (xs, ldx) at it; otherwise leave them at X.
+bool pad_needed(const Plan &p, const void *x) { return p.pad && !dma_rows(p.n, x); }
+
 int pad_input(const Plan &p, void *workspace, const void *x, int64_t batch, hipStream_t stream,
               const void *&xs, int64_t &ldx) {
-    if (!p.pad) return MUON_POLAR_OK;
+    if (!pad_needed(p, x)) return MUON_POLAR_OK;
     uint16_t *xp = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + p.pad_offset);
     const int st = finish_stage(
         muon_polar::launch_pad_rows(static_cast<const uint16_t *>(x), xp, batch * p.m, p.n, p.np,
@@ -1559,8 +1574,9 @@ int muon_polar_check_plan(int64_t batch, int64_t m, int64_t n, int cus, const in
     const uintptr_t kX = uintptr_t(2) << 44, kY = uintptr_t(3) << 44;
     const void *x = reinterpret_cast<const void *>(kX);
     void *y = reinterpret_cast<void *>(kY);
-    const void *xs = p.pad ? static_cast<const void *>(ws + p.pad_offset) : x;
-    const int64_t ldx = p.pad ? p.np : n;
+    const bool pad = pad_needed(p, x);
+    const void *xs = pad ? static_cast<const void *>(ws + p.pad_offset) : x;
+    const int64_t ldx = pad ? p.np : n;
     void *gram = ws;
     void *poly = ws + align256(p.gram_bytes);
     StageLaunch L[3] = {p.tall ? gram_t_launch(p, xs, ldx, gram, m, n) : gram_launch(p, xs, ldx, gram, m, n),

@@ -94,15 +94,16 @@ bool tile_supported(Stage s, int bm, int bn);
 hipError_t launch_gemm(Stage s, int bm, int bn, bool vec, const GemmArgs &g, int grid,
                        hipStream_t stream);
 
-// DMA-fed kernels: X chunks of 16 B must be entirely inside or outside the matrix
-// (n % 8 == 0, 16-byte aligned X).  Grid is g.sk_units + 8 * g.per_xcd; `waves`
-// per workgroup as returned by stream_waves; `depth` LDS ring slots (one K-step
-// each), a combination stream_depth_supported accepts.  k_mask (gram and
-// apply-right only): the K-contiguous operands' rows end inside the last K-step
-// (X rows of n % 64 != 0 elements read in place), so the K-masked variant loads
-// that step's chunks past row_k / col_k as zeros.
+// DMA-fed kernels: X rows of 16-byte chunks (n % 8 == 0, 16-byte aligned X) or of an
+// even number of elements from a 4-byte aligned X.  Grid is g.sk_units + 8 * g.per_xcd;
+// `waves` per workgroup as returned by stream_waves; `depth` LDS ring slots (one K-step
+// each), a combination stream_depth_supported accepts.  k_mask (gram and apply-right):
+// 1 = the K-contiguous operands' rows end inside the last K-step (X rows of n % 64 != 0
+// elements read in place), so the K-masked variant loads that step's chunks past row_k /
+// col_k as zeros; 2 (gram only) = as 1, rows of n % 8 != 0 elements: the chunk that
+// straddles n also has its positions past n zeroed in LDS.
 hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const GemmArgs &g,
-                         hipStream_t stream, bool k_mask = false);
+                         hipStream_t stream, int k_mask = 0);
 
 // Whether a DMA-fed kernel exists for (s, bm, bn, waves, depth).
 bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth);

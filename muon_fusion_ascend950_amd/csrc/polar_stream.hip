@@ -124,7 +124,7 @@ __device__ __forceinline__ void store16_cpol(int cpol, u32x4 v, __amdgpu_buffer_
 // the launch's 2*BN-wide tile grid (the apply stage's last round, see
 // polar_stream_halves_kernel).  DG: the unit is a pair of diagonal tiles
 // (GemmArgs::diag_pairs; tile (tm, tn) = (2p, 2p + 1) names its two panels).
-template <int BM, int BN, Stage S, int NW, int D, bool KT, bool DG = false>
+template <int BM, int BN, Stage S, int NW, int D, int KT, bool DG = false>
 __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem, uint16_t *sink,
                                                uint32_t *s_arrived_p, int unit, int tile_base,
                                                int lt, int kbeg, int kend, int half = -1) {
@@ -323,6 +323,57 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             dma_16B(rs_col, live ? b_dst(slot, i) : sink_base, off);
         }
     };
+    // KT with rows of n % 8 != 0 elements (gram reading X rows of even length in
+    // place, 4-byte aligned): on the tile's last K-step the chunk that holds K
+    // position n also holds the next row's first values (a matrix's last row:
+    // zeros past the buffer).  Once this lane's DMA of that step has landed, its
+    // positions >= n are zeroed in LDS before the step's barrier, so the operands
+    // hold the zeros a zero-padded copy of X holds there.  tail_rem packs, per DMA
+    // instruction d of this lane, the number of valid values (1..7) in its chunk of
+    // that step in bits 4d..4d+3 (0: nothing to zero).
+    static_assert(Geo::kLoads <= 16, "tail_rem holds 16 instructions");
+    const bool tail_fix = KT == 2 && ((g.row_k | g.col_k) & 7) != 0 && kend == nk;
+    uint64_t tail_rem = 0;
+    if constexpr (KT == 2) {
+        if (tail_fix) {
+            const int k0 = (nk - 1) * kBK;
+#pragma unroll
+            for (int d = 0; d < Geo::kLoads; ++d) {
+                const int rem = d < Geo::kLoadsA ? g.row_k - (k0 + 8 * a_chunk(d))
+                                                 : g.col_k - (k0 + 8 * b_chunk(d - Geo::kLoadsA));
+                if (rem > 0 && rem < kChunk) tail_rem |= uint64_t(rem) << (4 * d);
+            }
+        }
+    }
+    auto fix_tail = [&](int slot_) {
+        if constexpr (KT == 2) {
+            // an opaque copy of the wave index keeps this address arithmetic here
+            // rather than hoisted out of the K loop (where its values would stay
+            // live in scalar registers and spill)
+            int wv = wave;
+            asm volatile("" : "+s"(wv));
+            const uint32_t base = smem_base + slot_ * Geo::kStageBytes + 16 * lane;
+#pragma unroll
+            for (int d = 0; d < Geo::kLoads; ++d) {
+                const uint32_t dst =
+                    d < Geo::kLoadsA
+                        ? base + (wv * Geo::kLoadsA + d) * 1024
+                        : base + Geo::kABytes + (wv * Geo::kLoadsB + d - Geo::kLoadsA) * 1024;
+                // keep values 0 .. rem-1 of the chunk (all of it when rem is 0)
+                const int rem = static_cast<int>((tail_rem >> (4 * d)) & 15u);
+                u32x4 *q = reinterpret_cast<u32x4 *>(smem + (dst - smem_base) / 2);
+                u32x4 v = *q;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t keep = rem == 0 || 2 * w + 1 < rem ? 0xffffffffu
+                                          : 2 * w < rem              ? 0x0000ffffu
+                                                                     : 0u;
+                    v[w] &= keep;
+                }
+                *q = v;
+            }
+        }
+    };
     auto issue_all = [&](int step, int slot) {
 #pragma unroll
         for (int d = 0; d < Geo::kLoads; ++d) dma_one(d, step, slot, true);
@@ -507,6 +558,10 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     const int npro = nkl < kStages ? nkl : kStages;
     for (int i = 0; i < npro; ++i) issue_all(kbeg + i, i);
     int epi_slot = 0;
+    if (tail_fix && nkl == 1) {  // the segment is the tile's last K-step alone
+        wait_vm<0>();
+        fix_tail(0);
+    }
     if constexpr (kEpiPrefetch) {
         if (nkl < kStages) {
             epi_slot = nkl;  // a slot the K loop never fills
@@ -548,6 +603,10 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             __builtin_amdgcn_sched_barrier(0);
             // the waits of the schedule below (panel k+1; later DMA groups in flight)
             const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+            if (tail_fix && k == nkl - 2) {
+                wait_vm<0>();
+                fix_tail(next);
+            }
             wait_panels_barrier<Geo::kLoads, kStages - 1, kExtra>(after);
             mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
                                  fc0, ka);
@@ -591,6 +650,10 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             const int next = slot + 1 == kStages ? 0 : slot + 1;
             // the waits of the one-MFMA-per-slice schedule below
             const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+            if (tail_fix && k == nkl - 2) {
+                wait_vm<0>();
+                fix_tail(next);
+            }
             if (kEpiPrefetch && k > nkl - kStages)
                 wait_panels_barrier<Geo::kLoads, kStages - 1, kEpiLoadsU>(after);
             else
@@ -644,6 +707,10 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             // the same waits as the schedule below: panel k+1, before this
             // step's DMA group
             const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+            if (tail_fix && k == nkl - 2) {
+                wait_vm<0>();
+                fix_tail(next);
+            }
             if (kEpiPrefetch && k > nkl - kStages)
                 wait_panels_barrier<Geo::kLoads, kStages - 1, kEpiLoadsU>(after);
             else
@@ -717,6 +784,10 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             // counts on the join below assume none were issued, and the slice-3
             // MFMAs would then wait for all of them.
             const int after = (npro - k - 2 > 0 ? npro - k - 2 : 0) + (k < kStages - 2 ? k : kStages - 2);
+            if (tail_fix && k == nkl - 2) {
+                wait_vm<0>();
+                fix_tail(next);
+            }
             if (kEpiPrefetch && k > nkl - kStages)
                 wait_panels_barrier<Geo::kLoads, kStages - 1, kEpiLoadsU>(after);
             else
@@ -1063,7 +1134,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     }
 }
 
-template <int BM, int BN, Stage S, int NW, int D, bool KT>
+template <int BM, int BN, Stage S, int NW, int D, int KT>
 __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
     using Geo = StreamGeom<BM, BN, NW, D>;
     constexpr int kStages = Geo::kStages;
@@ -1112,7 +1183,7 @@ __global__ __launch_bounds__(64 * NW) void polar_stream_kernel(GemmArgs g) {
 // (g.sk_units = the number of halves, a multiple of 8; XCD-contiguous runs of
 // halves).  A half computes its whole K range: no partials, no fix-up.  The
 // halves run the wave-pair kernel (two K chains per output).
-template <Stage S, bool KT, int DH>
+template <Stage S, int KT, int DH>
 __global__ __launch_bounds__(512) void polar_stream_halves_kernel(GemmArgs g) {
     // ring: two 64 KiB slots for the whole tiles, DH 48 KiB slots for the halves
     constexpr int kWhole = 2 * StreamGeom<256, 256, 8, 2>::kStageBytes;
@@ -1154,13 +1225,13 @@ constexpr bool depth_ok(int waves, int depth) {
     return depth == 2;
 }
 
-template <int BM, int BN, Stage S, int NW, int D, bool KT>
+template <int BM, int BN, Stage S, int NW, int D, int KT>
 const void *kernel_ptr() {
     return reinterpret_cast<const void *>(&polar_stream_kernel<BM, BN, S, NW, D, KT>);
 }
 
 // Kernel of (BM, BN, S, KT) for the given waves and depth, or null.
-template <int BM, int BN, Stage S, bool KT>
+template <int BM, int BN, Stage S, int KT>
 const void *kernel_for(int waves, int depth) {
     if (!depth_ok<BM, BN>(waves, depth)) return nullptr;
     if constexpr (BM == 256 && BN == 256) {
@@ -1185,7 +1256,7 @@ const void *kernel_for(int waves, int depth) {
     }
 }
 
-template <Stage S, bool KT>
+template <Stage S, int KT>
 const void *kernel_by_tile(int bm, int bn, int waves, int depth) {
     if (bm == 64 && bn == 64) return kernel_for<64, 64, S, KT>(waves, depth);
     if (bm == 128 && bn == 128) return kernel_for<128, 128, S, KT>(waves, depth);
@@ -1201,20 +1272,22 @@ const void *kernel_by_tile(int bm, int bn, int waves, int depth) {
 }
 
 // kt: the K-masked variant (gram and apply-right only).
-const void *stream_kernel(Stage s, int bm, int bn, int waves, int depth, bool kt) {
+const void *stream_kernel(Stage s, int bm, int bn, int waves, int depth, int kt) {
     switch (s) {
         case Stage::Gram:
-            return kt ? kernel_by_tile<Stage::Gram, true>(bm, bn, waves, depth)
-                      : kernel_by_tile<Stage::Gram, false>(bm, bn, waves, depth);
+            return kt == 2   ? kernel_by_tile<Stage::Gram, 2>(bm, bn, waves, depth)
+                   : kt == 1 ? kernel_by_tile<Stage::Gram, 1>(bm, bn, waves, depth)
+                             : kernel_by_tile<Stage::Gram, 0>(bm, bn, waves, depth);
         case Stage::Poly:
-            return kt ? nullptr : kernel_by_tile<Stage::Poly, false>(bm, bn, waves, depth);
+            return kt ? nullptr : kernel_by_tile<Stage::Poly, 0>(bm, bn, waves, depth);
         case Stage::Apply:
-            return kt ? nullptr : kernel_by_tile<Stage::Apply, false>(bm, bn, waves, depth);
+            return kt ? nullptr : kernel_by_tile<Stage::Apply, 0>(bm, bn, waves, depth);
         case Stage::GramT:
-            return kt ? nullptr : kernel_by_tile<Stage::GramT, false>(bm, bn, waves, depth);
+            return kt ? nullptr : kernel_by_tile<Stage::GramT, 0>(bm, bn, waves, depth);
         case Stage::ApplyR:
-            return kt ? kernel_by_tile<Stage::ApplyR, true>(bm, bn, waves, depth)
-                      : kernel_by_tile<Stage::ApplyR, false>(bm, bn, waves, depth);
+            return kt == 1   ? kernel_by_tile<Stage::ApplyR, 1>(bm, bn, waves, depth)
+                   : kt == 0 ? kernel_by_tile<Stage::ApplyR, 0>(bm, bn, waves, depth)
+                             : nullptr;
     }
     return nullptr;
 }
@@ -1232,26 +1305,27 @@ bool stream_depth_supported(Stage s, int bm, int bn, int waves, int depth) {
 // The halves kernel of an apply stage (polar_stream_halves_kernel) with a ring of
 // `dh` slots for the halves (2 or 3), or null.
 template <int DH>
-const void *halves_kernel_d(Stage s, bool kt) {
+const void *halves_kernel_d(Stage s, int kt) {
     switch (s) {
         case Stage::Apply:
             return kt ? nullptr : reinterpret_cast<const void *>(
-                                      &polar_stream_halves_kernel<Stage::Apply, false, DH>);
+                                      &polar_stream_halves_kernel<Stage::Apply, 0, DH>);
         case Stage::ApplyR:
-            return kt ? reinterpret_cast<const void *>(
-                            &polar_stream_halves_kernel<Stage::ApplyR, true, DH>)
+            return kt == 2 ? nullptr
+                   : kt ? reinterpret_cast<const void *>(
+                            &polar_stream_halves_kernel<Stage::ApplyR, 1, DH>)
                       : reinterpret_cast<const void *>(
-                            &polar_stream_halves_kernel<Stage::ApplyR, false, DH>);
+                            &polar_stream_halves_kernel<Stage::ApplyR, 0, DH>);
         default:
             return nullptr;
     }
 }
-const void *halves_kernel(Stage s, bool kt, int dh) {
+const void *halves_kernel(Stage s, int kt, int dh) {
     return dh == 3 ? halves_kernel_d<3>(s, kt) : dh == 2 ? halves_kernel_d<2>(s, kt) : nullptr;
 }
 
 hipError_t launch_stream(Stage s, int bm, int bn, int waves, int depth, const GemmArgs &g,
-                         hipStream_t stream, bool k_mask) {
+                         hipStream_t stream, int k_mask) {
     if (g.halves) {
         // 256x256 whole tiles with 8 waves and two ring slots, then 256x128 halves
         const void *k = bm == 256 && bn == 256 && waves == 8 && depth == 2
