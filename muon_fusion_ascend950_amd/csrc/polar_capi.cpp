@@ -70,6 +70,8 @@ struct Knobs {
     uint32_t sk_rounds;     // per stage (bit 0 gram, bit 1 poly, bit 2 apply): a stream-K
                             // split of 256x256 tiles with a short last round also takes
                             // the whole round before it (sk_policy)
+    uint32_t sk_share;      // minimum K-steps per stream-K share (0: by tile size, sk_min_share)
+    uint32_t sk_pieces;     // most stream-K pieces per cut tile (0: by tile size, sk_max_pieces)
     uint32_t y_cpol, ap_cpol;  // cache policy of the DMA-fed kernels' Y / A and P stores
                                // (GemmArgs::out_cpol)
     bool operator==(const Knobs &o) const {
@@ -78,7 +80,7 @@ struct Knobs {
                waves == o.waves && depth[0] == o.depth[0] && depth[1] == o.depth[1] &&
                depth[2] == o.depth[2] && pair == o.pair && halves == o.halves &&
                halves_depth == o.halves_depth && diag_pairs == o.diag_pairs &&
-               sk_rounds == o.sk_rounds && y_cpol == o.y_cpol &&
+               sk_rounds == o.sk_rounds && sk_share == o.sk_share && sk_pieces == o.sk_pieces && y_cpol == o.y_cpol &&
                ap_cpol == o.ap_cpol;
     }
 };
@@ -115,7 +117,7 @@ struct PlanKeyHash {
         mix(k.knobs.halves_depth);
         mix(k.knobs.diag_pairs);
         mix(k.knobs.sk_rounds);
-        mix(uint64_t(k.knobs.y_cpol) << 8 | k.knobs.ap_cpol);
+        mix(uint64_t(k.knobs.sk_pieces) << 32 | uint64_t(k.knobs.sk_share) << 16 | uint64_t(k.knobs.y_cpol) << 8 | k.knobs.ap_cpol);
         return static_cast<size_t>(h);
     }
 };
@@ -276,6 +278,11 @@ int read_knobs(int64_t batch, int64_t m, int64_t n, int cus, Knobs &k) {
     // 37.9 -> 34.3, [2,2048,8192] 249.9 -> 244.1; single steps [8,512,2048] 34.7 ->
     // 34.2, [4096,14336] 671.7 -> 664.6 and 694.0 -> 690.9 (two boxes), [14336,4096]
     // 678.6 -> 672.5; [4,4096,4096] unchanged.
+    k.sk_share = static_cast<uint32_t>(env_u64("MUON_POLAR_SK_MIN_SHARE", 0));
+    if (k.sk_share > 4096) return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_SK_MIN_SHARE must be 0..4096");
+    k.sk_pieces = static_cast<uint32_t>(env_u64("MUON_POLAR_SK_PIECES", 0));
+    if (k.sk_pieces == 1 || k.sk_pieces > 16)
+        return fail(MUON_POLAR_ERR_CONFIG, "MUON_POLAR_SK_PIECES must be 0 (by tile) or 2..16");
     k.y_cpol = static_cast<uint32_t>(env_u64("MUON_POLAR_Y_CPOL", 2));
     k.ap_cpol = static_cast<uint32_t>(env_u64("MUON_POLAR_AP_CPOL", 2));
     if (k.y_cpol > 4 || k.ap_cpol > 4)
@@ -358,8 +365,8 @@ int check_shape(int64_t batch, int64_t m, int64_t n) {
 // Stream-K for the last round of a stage when it is well under full: with
 // `resident` workgroups in flight, T tiles take ceil(T / resident) rounds one
 // tile per workgroup.  The rem = T % resident tiles of the last round are cut
-// into about `pieces` shares of K-steps each (at most 3, and no more units than
-// resident workgroups), which makes the last round rem * pieces / resident of a
+// into about `pieces` shares of K-steps each (at most sk_max_pieces, and no more
+// units than resident workgroups), which makes the last round rem * pieces / resident of a
 // round plus the fixup: a tile's last contributor reads the other pieces'
 // partials, so pieces stay few.  Off when the last round is over 3/4 full, when
 // tiles would average under 1.5 pieces, or a share would be under min_share
@@ -377,21 +384,32 @@ int check_shape(int64_t batch, int64_t m, int64_t n) {
 // [1,1024,4096] unsplit 37.7 against 43.2 us per step in 408 units, [2,768,3072]
 // 35.9 against 44.1, [4,512,4096] 35.5 against 39.8; with one unit per CU the
 // split still wins ([1,512,8192] 35.0 against 42.9, [1,700,5000] 43.2 against 49.5,
-// [2,512,4096] 30.6 against 32.5).  64x64 tiles (16 KiB partials, 0.2 us K-steps)
-// need shares of 16 K-steps: [2,150,2050] unsplit 25.6 against 27.7 us with
-// shares of 12.
+// [2,512,4096] 30.6 against 32.5).  64x64 tiles (16 KiB partials, 0.2 us K-steps):
+// shares of 6 K-steps or more in up to four pieces (sk_max_pieces); three pieces of
+// 12 lose ([2,150,2050] unsplit 25.6 against 27.7 us).
 int64_t sk_min_share(int bm, int bn) {
     const int64_t area = int64_t(bm) * bn;
-    return area >= 256 * 256 ? 20 : (area <= 64 * 64 ? 16 : 8);
+    return area >= 256 * 256 ? 20 : (area <= 64 * 64 ? 6 : 8);
 }
+// Most pieces a cut tile is split into.  64x64 tiles (16 KiB partials): up to four
+// shares of 6 K-steps or more, which shortens the critical path of a long-K stage
+// over few tiles more than the extra partial read costs (interleaved A/B against
+// three shares of 16 or more, per step: [2,150,2050] 25.4 -> 24.6 us, [1,256,8192]
+// 30.8 -> 27.7, [4,128,4096] 24.7 -> 23.3, [1,512,8192] 35.1 -> 33.1,
+// [1,200,12000] 42.4 -> 35.5; three shares of 12: [2,150,2050] 26.5 us).  Larger
+// tiles: three.
+int64_t sk_max_pieces(int bm, int bn) { return int64_t(bm) * bn <= 64 * 64 ? 4 : 3; }
 
 SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident, int64_t cus,
-                  int64_t min_share, bool extra_round) {
+                  int64_t min_share, bool extra_round, int64_t pieces = 3) {
     SkSplit c{tiles, 0, 0, 0};
     if (!enabled || resident < 8) return c;
     const int64_t rem = tiles % resident;
     if (rem == 0 || rem * 4 > resident * 3 || rem * 4 > cus * 3) return c;
-    const int64_t units = std::min<int64_t>(resident, rem * 3) / 8 * 8;
+    int64_t units = std::min<int64_t>(resident, rem * pieces);
+    // pieces beyond three stop at one unit per CU
+    if (units > cus && rem * 3 <= cus) units = cus;
+    units = units / 8 * 8;
     if (units * 2 < rem * 3 || units < 8 || units > cus) return c;
     const int64_t iters = rem * k_steps;
     if (iters < min_share * units || iters >= (int64_t(1) << 31)) return c;
@@ -528,9 +546,11 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
                       : muon_polar::stream_blocks_per_cu(stages[s], tiles_bm[s], tiles_bn[s],
                                                          p.waves[s], p.depth[s]);
         p.sk[s] = sk_policy(sk_ok && occ > 0, grids[s], ksteps[s], int64_t(cus) * occ, cus,
-                            sk_min_share(tiles_bm[s], tiles_bn[s]),
+                            (knobs.sk_share ? int64_t(knobs.sk_share) : sk_min_share(tiles_bm[s], tiles_bn[s])),
                             s < 2 && (knobs.sk_rounds >> s & 1u) != 0 &&
-                                tiles_bm[s] * tiles_bn[s] >= 256 * 256);
+                                tiles_bm[s] * tiles_bn[s] >= 256 * 256,
+                            knobs.sk_pieces ? int64_t(knobs.sk_pieces)
+                                            : sk_max_pieces(tiles_bm[s], tiles_bn[s]));
         // Apply's cut round as 256x128 column halves, one per workgroup, where the
         // halves number between a half and a whole round of resident workgroups
         // (each half is then as long as a stream-K share, or shorter): the same
@@ -559,7 +579,7 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
         if (s == 2 && p.sk[s].sk_units > 0 && (knobs.sk_rounds >> 2 & 1u) != 0 &&
             tiles_bm[s] * tiles_bn[s] >= 256 * 256)
             p.sk[s] = sk_policy(true, grids[s], ksteps[s], int64_t(cus) * occ, cus,
-                                sk_min_share(tiles_bm[s], tiles_bn[s]), true);
+                                (knobs.sk_share ? int64_t(knobs.sk_share) : sk_min_share(tiles_bm[s], tiles_bn[s])), true);
         // A partial last round that stream-K leaves whole (its shares would be
         // too short) runs as halves too, where they fit one round.
         if (s == 2 && p.sk[s].sk_units == 0 && knobs.halves == 1 && sk_ok && occ > 0 &&
