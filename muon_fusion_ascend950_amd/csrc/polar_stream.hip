@@ -103,19 +103,6 @@ __device__ __forceinline__ int epi_offset(int row, int col) {
     return row * BN + (epi_pos<BN>(row, col >> 3) << 3) + (col & 7);
 }
 
-// 16-byte store with the cache policy `cpol` (GemmArgs::out_cpol): the policy bits
-// of the store instruction must be constants.
-__device__ __forceinline__ void store16_cpol(int cpol, u32x4 v, __amdgpu_buffer_rsrc_t rs,
-                                             uint32_t off) {
-    switch (cpol) {
-        case 1: __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 2); break;   // nt
-        case 2: __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 16); break;  // sc1
-        case 3: __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 18); break;  // nt sc1
-        case 4: __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 17); break;  // sc0 sc1
-        default: __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0); break;
-    }
-}
-
 // One segment of a workgroup's work: K-steps [kbeg, kend) of output tile
 // tile_base + lt (its stream-K fixup when the tile is cut, and its epilogue when
 // this workgroup completes it).  `smem`, `sink` and `s_arrived` are the caller's
@@ -182,20 +169,6 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // diagonal pair, which fill one ring slot)
     constexpr int kEpiLoadsU = DG ? 2 * Geo::kEpiLoads : Geo::kEpiLoads;
     static_assert(!DG || 2 * Geo::kTileBytes <= Geo::kStageBytes, "a pair's tiles fill one slot");
-    // Wave pairs of a stage that loads an epilogue tile (poly's 192x192 A tile, 72
-    // KiB: one and a half ring slots): the tile is fetched during the K loop, into
-    // the two slots the loop has stopped refilling once the second-to-last step's
-    // barrier has passed (rows 0 .. kSplitRows-1 fill one slot, the rest the first
-    // part of the other), so its round trip overlaps the last K-step and the
-    // halves' reduction (which then runs through the third slot) instead of
-    // following them.  Segments of fewer K-steps than ring slots load it after the
-    // reduction, contiguously from slot 0.
-    constexpr bool kPairEpiPre = kPair && kEpiLoad && D >= 3;
-    constexpr int kSplitRows = Geo::kStageBytes / (BN * 2);
-    constexpr int kSplitBlocks = Geo::kStageBytes / 1024;
-    static_assert(!kPairEpiPre || (Geo::kTileBytes <= 2 * Geo::kStageBytes &&
-                                   Geo::kStageBytes % (BN * 2) == 0),
-                  "the prefetched epilogue tile fills two ring slots by whole rows");
     static_assert((D - 1) * Geo::kLoads + kEpiLoadsU <= 63, "vmcnt range");
     // Fragment schedule: a whole K-step ahead for one MFMA per slice, else one slice.
     constexpr bool kStepFrags = kMfmaPerSlice == 1;
@@ -383,9 +356,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // (the tile may span several slots from slot 0), rows/cols outside the
     // matrix read as zero.  Diagonal pairs: both tiles, the second 8 KiB after
     // the first.
-    // LDS byte addresses of the epilogue tile's first kSplitRows rows and of the
-    // rest (contiguous unless the tile was prefetched into two ring slots).
-    auto issue_epi_to = [&](uint32_t dst_lo, uint32_t dst_hi) {
+    auto issue_epi = [&](int eslot) {
         if constexpr (kEpiLoad) {
             const i32x4 rs_epi = make_buffer_rsrc(g.epi + bt * g.sb_epi, g.bytes_epi);
             constexpr int kChunksPerRow = BN / 8;
@@ -405,16 +376,9 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
                 const uint32_t v = (gr < g.out_rows && gc < g.out_cols)
                                        ? static_cast<uint32_t>((gr * g.ld_epi + gc) * 2)
                                        : kOob;
-                const uint32_t dst = kPairEpiPre && blk >= kSplitBlocks
-                                         ? dst_hi + (blk - kSplitBlocks) * 1024
-                                         : dst_lo + blk * 1024;
-                dma_16B(rs_epi, dst, v);
+                dma_16B(rs_epi, smem_base + eslot * Geo::kStageBytes + blk * 1024, v);
             }
         }
-    };
-    auto issue_epi = [&](int eslot) {
-        const uint32_t lo = smem_base + eslot * Geo::kStageBytes;
-        issue_epi_to(lo, lo + kSplitBlocks * 1024);
     };
 
     // -------------------------------------------------------- main loop
@@ -574,11 +538,6 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     } else {
         wait_panels_barrier<Geo::kLoads, kStages>(npro - 1);
     }
-    // the epilogue tile's two ring slots when prefetched (kPairEpiPre): the slots
-    // of the last steps but one, (nkl - 3) and (nkl - 2) mod D
-    const bool epi_pre = kPairEpiPre && nkl >= kStages;
-    const int pre_lo = ((nkl - 3) % kStages + kStages) % kStages;
-    const int pre_hi = ((nkl - 2) % kStages + kStages) % kStages;
     int slot = 0;
     if constexpr (kPair) {
         // This wave's k16 slices of every K-step: ka = h and kb = h + 2, in the
@@ -588,10 +547,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
         const int ka = kh, kb = kh + 2;
         bf16x8 fr0[SM], fc0[SN], fr1[SM], fc1[SN];
         load_frags(0, ka, fr0, fc0);
-        // kExtra: DMA instructions issued after the last ring panel that the step's
-        // wait leaves in flight (the prefetched epilogue tile)
-        auto pair_step = [&](int k, auto extra_c) {
-            constexpr int kExtra = decltype(extra_c)::value;
+        for (int k = 0; k < nkl; ++k) {
             const int next = slot + 1 == kStages ? 0 : slot + 1;
             if constexpr (kAxInLoop) add_ax(slot, kbeg + k);
             load_frags(slot, kb, fr1, fc1);
@@ -607,24 +563,11 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
                 wait_vm<0>();
                 fix_tail(next);
             }
-            wait_panels_barrier<Geo::kLoads, kStages - 1, kExtra>(after);
+            wait_panels_barrier<Geo::kLoads, kStages - 1>(after);
             mfmas_with_dma_frags(fr1, fc1, kbeg + k + kStages, slot, k + kStages < nkl, next, fr0,
                                  fc0, ka);
             __builtin_amdgcn_sched_barrier(0);
             slot = next;
-        };
-        // with the epilogue tile prefetched, the last two steps run after the loop:
-        // once step nkl - 2's barrier has passed, no wave reads slots pre_lo and
-        // pre_hi again in this segment
-        const int nmain = epi_pre ? nkl - 2 : nkl;
-        for (int k = 0; k < nmain; ++k) pair_step(k, std::integral_constant<int, 0>{});
-        if constexpr (kPairEpiPre) {
-            if (epi_pre) {
-                pair_step(nkl - 2, std::integral_constant<int, 0>{});
-                issue_epi_to(smem_base + pre_lo * Geo::kStageBytes,
-                             smem_base + pre_hi * Geo::kStageBytes);
-                pair_step(nkl - 1, std::integral_constant<int, kEpiLoadsU>{});
-            }
         }
     } else if constexpr (DG) {
         // Fragments of one K-step, slices taken in the order s_i = (2h + i) mod 4:
@@ -801,13 +744,8 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             slot = next;
         }
     }
-    // All waves are done with the ring (and no DMA is outstanding; a prefetched
-    // epilogue tile may still be landing in its two slots, outside the third slot
-    // the halves' reduction uses: it is waited for before the epilogue).
-    if (epi_pre)
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-        wait_vm_barrier<0>();
+    // All waves are done with the ring (and no DMA is outstanding).
+    wait_vm_barrier<0>();
 
     // Diagonal pairs: wave h = 1's block (1,0) over slices 2-3 goes through the ring
     // ([32][33] floats per tile, in a slot the epilogue tile was not fetched into)
@@ -840,15 +778,10 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     // ring): f32x4 group e4 of block f of wave tile wq at [wq][f][e4][lane].
     if constexpr (kPair) {
         constexpr int kF = SM * SN;
-        // two rounds through the ring from slot 0; three rounds through one slot
-        // when the epilogue tile may occupy the other two (kPairEpiPre)
-        constexpr int kRounds = kPairEpiPre ? 3 : 2;
-        constexpr int kF0 = (kF + kRounds - 1) / kRounds;
-        static_assert(4 * kF0 * 4 * 64 * 16 <=
-                          (kPairEpiPre ? Geo::kStageBytes : kStages * Geo::kStageBytes),
+        constexpr int kF0 = (kF + 1) / 2;
+        static_assert(4 * kF0 * 4 * 64 * 16 <= kStages * Geo::kStageBytes,
                       "pair reduction buffer must fit the ring");
-        const int red_slot = epi_pre ? (nkl - 1) % kStages : 0;
-        f32x4 *buf = reinterpret_cast<f32x4 *>(smem + red_slot * (Geo::kStageBytes / 2));
+        f32x4 *buf = reinterpret_cast<f32x4 *>(smem);
         auto round = [&](auto lo_c, auto hi_c) {
             constexpr int lo = decltype(lo_c)::value, hi = decltype(hi_c)::value;
             if (kh == 1) {
@@ -876,13 +809,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         };
         round(std::integral_constant<int, 0>{}, std::integral_constant<int, kF0>{});
-        if constexpr (kRounds == 2) {
-            round(std::integral_constant<int, kF0>{}, std::integral_constant<int, kF>{});
-        } else {
-            static_assert(kRounds == 3 && 3 * kF0 >= kF && 2 * kF0 < kF, "three rounds");
-            round(std::integral_constant<int, kF0>{}, std::integral_constant<int, 2 * kF0>{});
-            round(std::integral_constant<int, 2 * kF0>{}, std::integral_constant<int, kF>{});
-        }
+        round(std::integral_constant<int, kF0>{}, std::integral_constant<int, kF>{});
     }
 
     // -------------------------------------------------------- stream-K fixup
@@ -964,7 +891,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
         // fetched now, so that its round trip overlaps the partials' reads
         // instead of following them.
         if constexpr (kEpiLoad && !kEpiPrefetch) {
-            if (!epi_pre) issue_epi(0);
+            issue_epi(0);
             epi_issued = true;
         }
         // Own partial first or second in the order: add the others to it in
@@ -1012,17 +939,9 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
 
     // -------------------------------------------------------- epilogue
     uint16_t *tile = smem + epi_slot * (Geo::kStageBytes / 2);
-    // rows kSplitRows.. of a tile prefetched into two ring slots sit in the second
-    uint16_t *tile_hi = epi_pre ? smem + pre_hi * (Geo::kStageBytes / 2) : tile + kSplitRows * BN;
-    if (epi_pre) tile = smem + pre_lo * (Geo::kStageBytes / 2);
     // element (row, col) of staged output tile ot
     auto at = [&](int ot, int row, int col) -> uint16_t * {
-        if constexpr (kPairEpiPre) {
-            uint16_t *rb = row < kSplitRows ? tile + row * BN : tile_hi + (row - kSplitRows) * BN;
-            return rb + (epi_pos<BN>(row, col >> 3) << 3) + (col & 7);
-        } else {
-            return tile + ot * (BM * BN) + epi_offset<BN>(row, col);
-        }
+        return tile + ot * (BM * BN) + epi_offset<BN>(row, col);
     };
     uint16_t *out = g.out + bt * g.sb_out;
     const __amdgpu_buffer_rsrc_t rs_out =
@@ -1031,7 +950,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     constexpr int kOutTiles = DG ? 2 : 1;  // staged [BM][BN] tiles, one after the other
 
     if constexpr (kEpiLoad && !kEpiPrefetch) {
-        if (!epi_issued && !epi_pre) issue_epi(0);
+        if (!epi_issued) issue_epi(0);
         wait_vm_barrier<0>();
     }
 
@@ -1066,65 +985,79 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    // Coalesced store of the tile: 16-byte chunks, consecutive threads along a row.
-    constexpr int kChunksPerRow = BN / 8;
-    for (int idx = tid; idx < kOutTiles * BM * kChunksPerRow; idx += kThreads) {
-        // diagonal pairs: tile ot of the two at (row0 + ot * BM, row0 + ot * BM)
-        const int ot = DG ? idx / (BM * kChunksPerRow) : 0;
-        const int ti = DG ? idx - ot * (BM * kChunksPerRow) : idx;
-        const int row = ti / kChunksPerRow, c = ti % kChunksPerRow;
-        const int sr0 = DG ? row0 + ot * BM : row0, sc0 = DG ? sr0 : col0;
-        const int gr = sr0 + row, gc = sc0 + 8 * c;
-        if constexpr (!Tr::kSymmetric) {
-            if (gr >= g.out_rows || gc >= g.out_cols) continue;
-        }
-        u32x4 v;
-        if (!diag) {
-            v = *reinterpret_cast<const u32x4 *>(at(ot, row, 8 * c));
-        } else {
-            // Diagonal tile: element (r, c) comes from the upper-triangle source
-            // min/max(r, c), so the stored matrix is bitwise symmetric.
-            uint32_t hh[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int col = 8 * c + e;
-                hh[e] = row <= col ? *at(ot, row, col) : *at(ot, col, row);
+    // The tile's stores, with the cache policy GemmArgs::out_cpol as the constant
+    // kAux of the store instructions (the switch below picks one instantiation).
+    auto store_out = [&](auto aux_c) {
+        constexpr int kAux = decltype(aux_c)::value;
+        auto st16 = [&](u32x4 v, int elem) {
+            __builtin_amdgcn_raw_buffer_store_b128(v, rs_out, static_cast<uint32_t>(elem * 2), 0,
+                                                   kAux);
+        };
+        // Coalesced store of the tile: 16-byte chunks, consecutive threads along a row.
+        constexpr int kChunksPerRow = BN / 8;
+        for (int idx = tid; idx < kOutTiles * BM * kChunksPerRow; idx += kThreads) {
+            // diagonal pairs: tile ot of the two at (row0 + ot * BM, row0 + ot * BM)
+            const int ot = DG ? idx / (BM * kChunksPerRow) : 0;
+            const int ti = DG ? idx - ot * (BM * kChunksPerRow) : idx;
+            const int row = ti / kChunksPerRow, c = ti % kChunksPerRow;
+            const int sr0 = DG ? row0 + ot * BM : row0, sc0 = DG ? sr0 : col0;
+            const int gr = sr0 + row, gc = sc0 + 8 * c;
+            if constexpr (!Tr::kSymmetric) {
+                if (gr >= g.out_rows || gc >= g.out_cols) continue;
             }
-            v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
-                      hh[6] | (hh[7] << 16)};
-        }
-        if (Tr::kSymmetric) {
-            store16_cpol(g.out_cpol, v, rs_out, static_cast<uint32_t>((gr * g.ld_out + gc) * 2));
-        } else if (g.out_vec) {
-            // Y is not read again by this step: a non-temporal store keeps it from
-            // displacing operand panels in L2 ([8,512,2048] 46.8 -> 44.4 us; the
-            // large shapes unchanged; A and P, read by the next stage, stay cached)
-            store16_cpol(g.out_cpol, v, rs_out, static_cast<uint32_t>((gr * g.ld_out + gc) * 2));
-        } else {
-            // rows of n % 8 != 0 elements: 2-byte stores up to the last column
-            uint16_t *dst = out + gr * g.ld_out + gc;
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (gc + e < g.out_cols) dst[e] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
-        }
-    }
-
-    // Mirrored store (symmetric stages, off-diagonal tiles): row c of the
-    // mirror tile is column c of this tile; consecutive threads walk along it.
-    if constexpr (Tr::kSymmetric) {
-        if (!diag) {
-            constexpr int kMirrorChunks = BM / 8;  // 16-byte chunks per mirror row
-            for (int idx = tid; idx < BN * kMirrorChunks; idx += kThreads) {
-                const int mc = idx / kMirrorChunks, rb = idx % kMirrorChunks;
+            u32x4 v;
+            if (!diag) {
+                v = *reinterpret_cast<const u32x4 *>(at(ot, row, 8 * c));
+            } else {
+                // Diagonal tile: element (r, c) comes from the upper-triangle source
+                // min/max(r, c), so the stored matrix is bitwise symmetric.
                 uint32_t hh[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) hh[e] = *at(0, 8 * rb + e, mc);
-                const u32x4 v{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16),
-                              hh[4] | (hh[5] << 16), hh[6] | (hh[7] << 16)};
-                store16_cpol(g.out_cpol, v, rs_out,
-                             static_cast<uint32_t>(((col0 + mc) * g.ld_out + row0 + 8 * rb) * 2));
+                for (int e = 0; e < 8; ++e) {
+                    const int col = 8 * c + e;
+                    hh[e] = row <= col ? *at(ot, row, col) : *at(ot, col, row);
+                }
+                v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
+                          hh[6] | (hh[7] << 16)};
+            }
+            if (Tr::kSymmetric || g.out_vec) {
+                st16(v, gr * g.ld_out + gc);
+            } else {
+                // rows of n % 8 != 0 elements: 2-byte stores up to the last column
+                uint16_t *dst = out + gr * g.ld_out + gc;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (gc + e < g.out_cols)
+                        dst[e] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
             }
         }
+
+        // Mirrored store (symmetric stages, off-diagonal tiles): row c of the
+        // mirror tile is column c of this tile; consecutive threads walk along it.
+        if constexpr (Tr::kSymmetric) {
+            if (!diag) {
+                constexpr int kMirrorChunks = BM / 8;  // 16-byte chunks per mirror row
+                for (int idx = tid; idx < BN * kMirrorChunks; idx += kThreads) {
+                    const int mc = idx / kMirrorChunks, rb = idx % kMirrorChunks;
+                    uint32_t hh[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) hh[e] = *at(0, 8 * rb + e, mc);
+                    const u32x4 v{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16),
+                                  hh[4] | (hh[5] << 16), hh[6] | (hh[7] << 16)};
+                    st16(v, (col0 + mc) * g.ld_out + row0 + 8 * rb);
+                }
+            }
+        }
+    };
+    switch (g.out_cpol) {
+        case 1: store_out(std::integral_constant<int, 2>{}); break;   // nt
+        case 2: store_out(std::integral_constant<int, 16>{}); break;  // sc1
+        case 3: store_out(std::integral_constant<int, 18>{}); break;  // nt sc1
+        case 4: store_out(std::integral_constant<int, 17>{}); break;  // sc0 sc1
+        default: store_out(std::integral_constant<int, 0>{}); break;
+    }
+
+    if constexpr (Tr::kSymmetric) {
         if constexpr (DG) {
             zero_past_grid<BM>(g, out, tm, tm, tid, kThreads);
             zero_past_grid<BM>(g, out, tm + 1, tm + 1, tid, kThreads);
