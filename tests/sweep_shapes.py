@@ -1,0 +1,52 @@
+"""Shapes of the seeded polar_step sweep (tests/test_shape_sweep_gpu.py), shared with the
+CPU plan check (tests/test_plan_extents.py), which walks each shape's launch plan before
+any GPU run of it."""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def sweep_shapes(count: int = 32, seed: int = 2026):
+    rng = np.random.default_rng(seed)
+    shapes = []
+    for i in range(count):
+        width_class = i % 4  # odd, even (not 8), multiple of 8 (not 64), multiple of 64
+        short = int(rng.integers(1, 1100))
+        long_ = short + int(rng.integers(0, 2400))
+        if width_class == 0:
+            long_ |= 1
+        elif width_class == 1:
+            long_ = long_ - long_ % 8 + int(rng.choice([2, 4, 6]))
+        elif width_class == 2:
+            long_ = max(8, long_ - long_ % 8)
+            if long_ % 64 == 0:
+                long_ += 8
+        else:
+            long_ = max(64, long_ - long_ % 64)
+        long_ = max(long_, short)
+        batch = int(rng.choice([1, 1, 2, 3]))
+        tall = rng.random() < 0.3 and short < long_
+        if tall:
+            # M > N: the width class describes N (the short side, the rows' length)
+            n = short if width_class != 3 else max(64, short - short % 64)
+            if width_class == 0:
+                n |= 1
+            elif width_class == 1:
+                n = max(2, n - n % 8 + 2)
+            elif width_class == 2:
+                n = max(8, n - n % 8)
+                if n % 64 == 0:
+                    n += 8
+            m = max(long_, n + 1)
+            shapes.append((batch, m, n))
+        else:
+            shapes.append((batch, short, long_))
+    return shapes
+
+
+
+def plan_shape(batch: int, m: int, n: int):
+    """The (batch, m, n) the C ABI plans for: M > N with N % 8 != 0 reaches it transposed
+    (the reference's wrapper route), every other shape as given."""
+    return (batch, n, m) if m > n and n % 8 != 0 else (batch, m, n)

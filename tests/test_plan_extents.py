@@ -17,6 +17,7 @@ from __future__ import annotations
 import pytest
 
 from muon_fusion_ascend950_amd import capi
+from tests.sweep_shapes import plan_shape, sweep_shapes
 
 BASELINE_SHAPES = [(4, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (8, 512, 2048),
                    (2, 150, 2050), (1, 129, 130)]
@@ -68,6 +69,13 @@ def test_baseline_plans_store_inside_their_buffers(shape, occ):
 @pytest.mark.parametrize("shape", MORE_SHAPES)
 def test_other_plans_store_inside_their_buffers(shape, occ):
     check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
+
+
+@pytest.mark.parametrize("occ", [(1, 1, 1), (2, 2, 2)])
+@pytest.mark.parametrize("shape", sweep_shapes())
+def test_sweep_plans_store_inside_their_buffers(shape, occ):
+    """The shapes of the GPU sweep (tests/test_shape_sweep_gpu.py), checked here first."""
+    check(capi.check_plan(*plan_shape(*shape), cus=256, blocks_per_cu=occ))
 
 
 @pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)])
