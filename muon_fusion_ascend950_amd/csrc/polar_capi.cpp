@@ -156,11 +156,13 @@ struct Plan {
     bool sk_any;
     int64_t counter_stride;
     size_t counters_offset, partials_offset;
-    // n % 8 != 0: each step first copies X into a zero-padded [batch, m, np]
-    // buffer (np = roundup(n, 64)) at pad_offset, which the DMA-fed kernels read
-    // (their panels are 16-byte chunks, which rows of n % 8 != 0 elements do not
-    // align to); Y is stored at its own width (2-byte stores).  Rows of
-    // n % 8 == 0 elements are read in place, a last K-step past n masked.
+    // n % 8 != 0: the workspace holds a zero-padded [batch, m, np] buffer
+    // (np = roundup(n, 64)) at pad_offset.  A step whose X the DMA-fed kernels
+    // cannot read in place (odd n, or X not 4-byte aligned: their panels are
+    // 16-byte chunks at 4-byte aligned addresses) first copies X into it and
+    // reads the copy; Y is stored at its own width (2-byte stores).  Rows of
+    // n % 8 == 0 elements, and of an even n from a 4-byte aligned X, are read in
+    // place, a last K-step past n masked (dma_rows).
     bool pad;
     int64_t np;
     size_t pad_offset;
@@ -1056,8 +1058,9 @@ int pad_input(const Plan &p, void *workspace, const void *x, int64_t batch, hipS
     return MUON_POLAR_OK;
 }
 
-// One step given the workspace: left form (m <= n) or right-Gram form; rows of
-// n % 8 != 0 elements are first copied into the zero-padded buffer.
+// One step given the workspace: left form (m <= n) or right-Gram form; rows the
+// DMA-fed kernels cannot read in place are first copied into the zero-padded
+// buffer (pad_input).
 int run_step(const Plan &p, const void *x, void *y, void *workspace, int64_t batch, double a,
              double b, double c, hipStream_t stream) {
     char *ws = static_cast<char *>(workspace);
@@ -1325,7 +1328,8 @@ int muon_polar_gram(const void *x, void *gram, void *workspace, size_t workspace
     const SkArea *ap = nullptr;
     st = stage_area(p, workspace, workspace_bytes, 0, area, ap);
     if (st != MUON_POLAR_OK) return st;
-    // with the step's workspace, the step's route (padded copy for n % 8 != 0)
+    // with the step's workspace, the step's route (the padded copy where pad_input
+    // takes it)
     const void *xs = x;
     int64_t ldx = n;
     if (ap != nullptr) {

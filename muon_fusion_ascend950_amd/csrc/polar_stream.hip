@@ -24,9 +24,11 @@
 //     contiguous run of tiles that share operand panels in its L2 (apply: runs
 //     of column tiles walked row by row; gram and poly: super-blocks of tiles).
 //
-// Used when every 16-byte chunk of X is either fully inside or fully outside
-// the matrix (n % 8 == 0, 16-byte aligned X and Y); the register-staged kernels
-// cover the rest.
+// Used when X's rows can be read as 16-byte chunks: n % 8 == 0 with X 16-byte
+// aligned, or an even n with X 4-byte aligned (the chunk that straddles a row's
+// end is masked; see KT below); odd rows reach these kernels through a
+// zero-padded copy, and the register-staged kernels cover calls without room
+// for one.
 #include "polar_epilogue.hpp"
 #include "polar_kernels.h"
 #include "polar_schedule.hpp"
@@ -268,15 +270,16 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
     };
     // DMA instruction d (0 .. kLoads-1) of K-step `step` into `slot`, or, when
     // `live` is false, out-of-range zeros into this wave's sink block (the same
-    // instruction, chosen by scalar operands).  No K masks: the host passes
-    // K-contiguous operands whose rows extend to a multiple of 64 elements with
-    // zeros (padded copies of X, padded A and P), and N-contiguous operands end
-    // at their buffer's num_records, past which the hardware returns zeros.
+    // instruction, chosen by scalar operands).  Without KT, K-contiguous operands
+    // have rows that extend to a multiple of 64 elements with zeros (A and P, a
+    // padded copy of X, or X with n % 64 == 0), and N-contiguous operands end at
+    // their buffer's num_records, past which the hardware returns zeros.
     // (An idle instruction whose row is outside the matrix wraps to offset 0:
     // an in-range read, also into the sink.)
     const uint32_t sink_base = lds_addr(sink) + wave * 1024;
-    // KT (gram and apply-right reading X rows of n % 64 != 0, n % 8 == 0
-    // elements in place): chunks at K positions past the operand's K extent
+    // KT (gram and apply-right reading X rows of n % 64 != 0 elements in place;
+    // KT == 2, below, also covers an even n % 8 != 0): chunks at K positions past
+    // the operand's K extent
     // (row_k, col_k; only in the last K-step) take an out-of-range offset, so
     // they read the zeros a padded copy of X would hold there, and the sums are
     // the padded copy's bit for bit.
