@@ -36,12 +36,14 @@
  * terms in two interleaved chains (wave pairs): they equal the one-chain kernels
  * to fp32 rounding.
  *
- * Rows of n % 8 != 0 elements: each step first copies X into a zero-padded
- * [batch, m, roundup(n, 64)] buffer at the end of the workspace, so that the
- * DMA-fed kernels (16-byte global->LDS transfers) serve every width; Y is
- * written at its own width (2-byte stores).  Rows of n % 8 == 0 elements are
- * read in place, the chunks of a last K-step past n masked to zeros (the same
- * sums as the padded copy, bit for bit).  Shapes whose padded copy would reach
+ * Widths: the DMA-fed kernels read X in place when its rows are n % 8 == 0
+ * elements from a 16-byte aligned X, or an even n from a 4-byte aligned X (16-byte
+ * global->LDS transfers at 4-byte aligned addresses); the chunks of a last K-step
+ * past n are masked to zeros (the same sums as a zero-padded X, bit for bit).
+ * Otherwise (odd n, or X not 4-byte aligned) each step first copies X into a
+ * zero-padded [batch, m, roundup(n, 64)] buffer at the end of the workspace, which
+ * info.workspace_bytes includes for every n % 8 != 0.  Y is written at its own
+ * width (2-byte stores when n % 8 != 0).  Shapes whose padded copy would reach
  * 2^30 elements per matrix are rejected ("matrix too large"), like X itself.
  *
  * Buffers: x, y and the workspace must be pairwise disjoint (no in-place call:
@@ -125,8 +127,8 @@ int muon_polar_step_noalloc(const void *x, void *y, int64_t batch, int64_t m, in
 /* The three stages one at a time.  `workspace` is NULL (workspace_bytes
  * ignored: the stage runs one output tile per workgroup) or a buffer of
  * info.workspace_bytes, the same one muon_polar_step takes (gram / poly may be
- * its A / P areas), which lets the stage use the stream-K split (and, for
- * n % 8 != 0, the padded copy of X) exactly as inside muon_polar_step, so the
+ * its A / P areas), which lets the stage use the stream-K split (and, where the
+ * step takes it, the padded copy of X) exactly as inside muon_polar_step, so the
  * three calls reproduce the step bit for bit.  The reference's stage launchers
  * likewise take a device-side buffer (their tiling struct).  The stages take
  * m <= n only. */
