@@ -131,7 +131,11 @@ int muon_polar_step_noalloc(const void *x, void *y, int64_t batch, int64_t m, in
  * step takes it, the padded copy of X) exactly as inside muon_polar_step, so the
  * three calls reproduce the step bit for bit.  The reference's stage launchers
  * likewise take a device-side buffer (their tiling struct).  The stages take
- * m <= n only. */
+ * m <= n only.  A stage's output must not overlap its inputs (every output tile
+ * reads whole rows of them while other tiles are stored), and no operand may
+ * overlap the workspace past its A and P areas (the arrival words, partial
+ * slots and padded copy of X the stage writes); MUON_POLAR_ERR_INVALID_ARGUMENT
+ * otherwise, before any launch. */
 
 /* Stage 1: gram[bt] = X[bt]·X[bt]ᵀ into a [batch, padded_rows, padded_rows]
  * bf16 buffer (padding written as zeros).
@@ -158,7 +162,8 @@ int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
  * X / (‖X‖_F·1.01 + 1e-6) with the rounding points of the reference recipe
  * (bf16 norm, bf16 product and sum, fp32 division rounded to bf16).
  * coefficients: `steps` triples (a, b, c), step i uses coefficients[3i..3i+2].
- * `workspace` must hold info.express_workspace_bytes; x and y must not overlap;
+ * `workspace` must hold info.express_workspace_bytes; x, y and the workspace
+ * must be pairwise disjoint;
  * steps >= 1, or steps == 0 with normalize (y = normalised x); m > n as for
  * muon_polar_step.
  * No reference counterpart: replaces the caller-side loop of the reference's

@@ -682,6 +682,16 @@ bool overlaps(const void *a, size_t a_bytes, const void *b, size_t b_bytes) {
     return x < y + b_bytes && y < x + a_bytes;
 }
 
+// Whether [buf, buf + bytes) shares a byte with the part of a stage call's workspace
+// that the call writes besides its output: the stream-K arrival words, the partial
+// slots and the padded copy of X (bytes [counters_offset, workspace_bytes)).  The A and
+// P areas before it may be the caller's gram and poly buffers.
+bool overlaps_stage_area(const Plan &p, const void *workspace, const void *buf, size_t bytes) {
+    if (workspace == nullptr) return false;
+    const char *area = static_cast<const char *>(workspace) + p.counters_offset;
+    return overlaps(area, p.workspace_bytes - p.counters_offset, buf, bytes);
+}
+
 // Workspace areas of polar_step's stream-K splits (null when not splitting:
 // the stage entry points have no workspace and run one tile per workgroup).
 struct SkArea {
@@ -1328,6 +1338,14 @@ int muon_polar_gram(const void *x, void *gram, void *workspace, size_t workspace
     const SkArea *ap = nullptr;
     st = stage_area(p, workspace, workspace_bytes, 0, area, ap);
     if (st != MUON_POLAR_OK) return st;
+    // every gram tile reads X's whole K range while other tiles are stored
+    const size_t x_bytes = static_cast<size_t>(batch * m * n * 2);
+    if (overlaps(x, x_bytes, gram, p.gram_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "x and gram must not overlap");
+    if (overlaps_stage_area(p, workspace, x, x_bytes) ||
+        overlaps_stage_area(p, workspace, gram, p.gram_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
+                    "x and gram must not overlap the workspace past its A and P areas");
     // with the step's workspace, the step's route (the padded copy where pad_input
     // takes it)
     const void *xs = x;
@@ -1354,6 +1372,13 @@ int muon_polar_poly(const void *gram, void *poly, void *workspace, size_t worksp
     const SkArea *ap = nullptr;
     st = stage_area(p, workspace, workspace_bytes, 1, area, ap);
     if (st != MUON_POLAR_OK) return st;
+    // every poly tile reads whole rows of A while other tiles are stored
+    if (overlaps(gram, p.gram_bytes, poly, p.gram_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "gram and poly must not overlap");
+    if (overlaps_stage_area(p, workspace, gram, p.gram_bytes) ||
+        overlaps_stage_area(p, workspace, poly, p.gram_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
+                    "gram and poly must not overlap the workspace past its A and P areas");
     return run_poly(p, gram, poly, batch, b, c, ap, stream);
 }
 
@@ -1378,6 +1403,11 @@ int muon_polar_apply(const void *poly, const void *x, void *y, void *workspace,
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "x and y must not overlap");
     if (overlaps(poly, p.gram_bytes, y, xy_bytes))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "poly and y must not overlap");
+    if (overlaps_stage_area(p, workspace, poly, p.gram_bytes) ||
+        overlaps_stage_area(p, workspace, x, xy_bytes) ||
+        overlaps_stage_area(p, workspace, y, xy_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT,
+                    "poly, x and y must not overlap the workspace past its A and P areas");
     const void *xs = x;
     int64_t ldx = n;
     if (ap != nullptr) {
@@ -1471,6 +1501,10 @@ int muon_polar_express(const void *x, void *y, void *workspace, size_t workspace
     const size_t xy_bytes = static_cast<size_t>(batch * m * n * 2);
     if (overlaps(x, xy_bytes, y, xy_bytes))
         return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "x and y must not overlap");
+    // the workspace holds A, P, the iterates between y's and the norm's partial sums
+    if (overlaps(workspace, p.express_workspace_bytes, x, xy_bytes) ||
+        overlaps(workspace, p.express_workspace_bytes, y, xy_bytes))
+        return fail(MUON_POLAR_ERR_INVALID_ARGUMENT, "the workspace must not overlap x or y");
     if (p.tall && steps > 0) {
         st = check_tall(p, x, y);
         if (st != MUON_POLAR_OK) return st;

@@ -398,3 +398,34 @@ def test_noalloc_rejects_shapes_beyond_its_scratch_before_any_launch():
     assert "muon_polar_step_noalloc holds" in capi.last_error()
     # a null x or y is refused first
     assert lib.muon_polar_step_noalloc(None, 16, 1, 8, 8, 1.0, 1.0, 1.0, None) == capi.ERR_INVALID_ARGUMENT
+
+
+def test_stage_calls_reject_overlapping_buffers_before_any_launch():
+    """The stage entry points and muon_polar_express refuse an output over one of
+    their inputs, and operands over the part of the workspace the call writes besides
+    its output (arrival words, partial slots, padded copy of X), before any device
+    call: the stand-in addresses below are never dereferenced."""
+    lib = capi.load()
+    batch, m, n = 2, 150, 2050
+    info = capi.query(batch, m, n)
+    wsb = info.workspace_bytes
+    stage_area = 2 * (-(-info.gram_bytes // 256) * 256)  # past the A and P areas
+    W, X, Y, G, P = (k << 40 for k in (1, 2, 3, 4, 5))
+    bad = capi.ERR_INVALID_ARGUMENT
+    # gram over x; x or gram in the workspace's stage area
+    assert lib.muon_polar_gram(X, X + 4096, None, 0, batch, m, n, None) == bad
+    assert "x and gram" in capi.last_error()
+    assert lib.muon_polar_gram(W + stage_area, G, W, wsb, batch, m, n, None) == bad
+    assert lib.muon_polar_gram(X, W + stage_area, W, wsb, batch, m, n, None) == bad
+    # poly in place; poly in the stage area
+    assert lib.muon_polar_poly(G, G, None, 0, batch, m, n, 1.0, 1.0, None) == bad
+    assert "gram and poly" in capi.last_error()
+    assert lib.muon_polar_poly(G, W + stage_area, W, wsb, batch, m, n, 1.0, 1.0, None) == bad
+    # apply with y in the stage area, or x there (the padded copy is written there)
+    assert lib.muon_polar_apply(P, X, W + stage_area, W, wsb, batch, m, n, 1.0, None) == bad
+    assert lib.muon_polar_apply(P, W + stage_area, Y, W, wsb, batch, m, n, 1.0, None) == bad
+    # express: the workspace over y
+    coeffs = (ctypes.c_double * 3)(1.0, 1.0, 1.0)
+    ews = info.express_workspace_bytes
+    assert lib.muon_polar_express(X, W + 4096, W, ews, batch, m, n, coeffs, 1, 1, None) == bad
+    assert "workspace must not overlap" in capi.last_error()
