@@ -79,7 +79,9 @@ def polar_step(x: torch.Tensor, a: float, b: float, c: float) -> torch.Tensor:
     tall = work.size(-2) > work.size(-1)
     if tall and work.size(-1) % 8 == 0:
         # M > N in the right-Gram form Y = a·X + X·(b·G + c·G²), G = XᵀX: the same
-        # step without the two transposed copies (equal to them bit for bit)
+        # step without the two transposed copies (equal to them bit for bit when no
+        # stage is cut by stream-K; to bf16 precision otherwise, since which tiles are
+        # cut follows each form's tile order)
         out = torch.ops.muon_ascend950.polar_step_tall(work, float(a), float(b), float(c))
         return out.squeeze(0) if squeeze_batch else out
     transposed = tall
