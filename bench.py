@@ -307,6 +307,27 @@ def sustained(fn, seconds: float) -> tuple:
 MUON_LR, MUON_MOMENTUM, MUON_WD = 0.02, 0.95, 0.01
 
 
+# One Muon optimizer step over two transformer layers' matrices at d = 768 (attention
+# q, k, v, o [768,768]; MLP [3072,768] and [768,3072]): small matrices, each of whose
+# steps leaves most CUs idle
+OPT_SHAPES = [(768, 768)] * 8 + [(3072, 768)] * 2 + [(768, 3072)] * 2
+
+
+def optimizer_step_us(grouped: bool) -> float:
+    """µs per Muon.step over OPT_SHAPES: one native update per parameter
+    (grouped=False) or same-shape parameters batched into one (Muon's default)."""
+    import torch
+    import muon_fusion_ascend950_amd as mf
+
+    gen = torch.Generator().manual_seed(3)
+    params = [torch.nn.Parameter((torch.randn(s, generator=gen) * 0.02).cuda()) for s in OPT_SHAPES]
+    for prm in params:
+        prm.grad = (torch.randn(prm.shape, generator=gen) * 1e-3).cuda()
+    opt = mf.Muon(params, lr=MUON_LR, momentum=MUON_MOMENTUM, weight_decay=MUON_WD,
+                  group_shapes=grouped)
+    return time_calls(opt.step, 10, 3) * 1e6
+
+
 def muon_tensors(m: int, n: int):
     """fp32 parameter, gradient and momentum buffer of one [m, n] matrix on the GPU."""
     import torch
@@ -621,6 +642,7 @@ def main() -> int:
                                                  weight_decay=MUON_WD), 10, 3)
     sec_muon_eager = time_calls(lambda: muon_eager_step(p, g, buf, mf.COEFFICIENTS), 5, 2)
     del p, g, buf
+    opt_single_us, opt_grouped_us = optimizer_step_us(False), optimizer_step_us(True)
 
     # PyTorch eager on the same GPU (the reference's comparison point, README.md:172-208)
     eager = time_calls(lambda: torch_formula(x, [COEFFS]), 10, 3)
@@ -685,6 +707,13 @@ def main() -> int:
             "torch_eager_us": round(sec_muon_eager * 1e6, 2),
             "speedup_vs_torch_eager": round(sec_muon_eager / sec_muon, 3),
             "elementwise_us": round((sec_muon - sec_express) * 1e6, 2),
+        },
+        "muon_optimizer": {
+            "workload": ("one Muon.step over 12 fp32 matrices (two layers at d = 768: 8 x "
+                         "[768,768], 2 x [3072,768], 2 x [768,3072]), 5 steps each"),
+            "one_call_per_parameter_us": round(opt_single_us, 2),
+            "same_shape_batched_us": round(opt_grouped_us, 2),
+            "speedup": round(opt_single_us / opt_grouped_us, 3),
         },
         "secondary": {
             "workload": "polar_step on bf16 [8,512,2048], one step",

@@ -23,6 +23,13 @@ import torch
 
 from .ops import COEFFICIENTS
 
+# Muon.step batches parameters of one shape into one native call when each matrix is
+# small (at most _GROUP_MAX_NUMEL elements): a small matrix alone leaves most CUs idle
+# and its steps are latency-bound, while a batch of them runs in about the time of one.
+# Batches hold at most _GROUP_BATCH_NUMEL elements (bounding the stacked copies).
+_GROUP_MAX_NUMEL = 1 << 22
+_GROUP_BATCH_NUMEL = 1 << 24
+
 
 def default_lr_scale(rows: int, cols: int) -> float:
     """nanochat's shape factor of the learning rate: sqrt(max(1, rows / cols))."""
@@ -101,10 +108,18 @@ class Muon(torch.optim.Optimizer):
     weight decay and the coefficient triples of the iteration (default: the
     reference's five).  Parameters must be float32 matrices (ndim >= 2) on the GPU;
     the momentum buffer is float32, created at the first step.
+
+    ``group_shapes``: parameters of one group that share a shape and a device, each of
+    at most 4M elements, are stacked and updated in one batched call (as nanochat's
+    Muon stacks same-shape parameters), in batches of at most 16M elements; each is
+    updated exactly as alone except that the batch's launch plan may cut the
+    iteration's sums differently (fp32 rounding of O; the momentum buffers are the
+    same bits).
     """
 
     def __init__(self, params, lr: float = 0.02, momentum: float = 0.95, nesterov: bool = True,
-                 ns_steps: int = 5, weight_decay: float = 0.0, coefficients=COEFFICIENTS):
+                 ns_steps: int = 5, weight_decay: float = 0.0, coefficients=COEFFICIENTS,
+                 group_shapes: bool = True):
         if lr < 0.0:
             raise ValueError(f"invalid learning rate {lr}")
         if not 0.0 <= momentum <= 1.0:
@@ -117,6 +132,7 @@ class Muon(torch.optim.Optimizer):
         defaults = dict(lr=lr, momentum=momentum, nesterov=nesterov, ns_steps=ns_steps,
                         weight_decay=weight_decay, coefficients=tuple(coefficients))
         super().__init__(params, defaults)
+        self.group_shapes = bool(group_shapes)
 
     @torch.no_grad()
     def step(self, closure=None):
@@ -125,6 +141,10 @@ class Muon(torch.optim.Optimizer):
             with torch.enable_grad():
                 loss = closure()
         for group in self.param_groups:
+            kw = dict(lr=group["lr"], momentum=group["momentum"], nesterov=group["nesterov"],
+                      weight_decay=group["weight_decay"], ns_steps=group["ns_steps"],
+                      coefficients=group["coefficients"])
+            batches = {}
             for p in group["params"]:
                 if p.grad is None:
                     continue
@@ -132,8 +152,31 @@ class Muon(torch.optim.Optimizer):
                 if "momentum_buffer" not in state:
                     state["momentum_buffer"] = torch.zeros_like(
                         p, dtype=torch.float32, memory_format=torch.contiguous_format)
-                muon_update(p, p.grad, state["momentum_buffer"], lr=group["lr"],
-                            momentum=group["momentum"], nesterov=group["nesterov"],
-                            weight_decay=group["weight_decay"], ns_steps=group["ns_steps"],
-                            coefficients=group["coefficients"])
+                if not self.group_shapes or p.numel() > _GROUP_MAX_NUMEL:
+                    muon_update(p, p.grad, state["momentum_buffer"], **kw)
+                    continue
+                key = (tuple(p.shape), p.device)
+                batch = batches.setdefault(key, [[]])
+                if batch[-1] and (len(batch[-1]) + 1) * p.numel() > _GROUP_BATCH_NUMEL:
+                    batch.append([])
+                batch[-1].append(p)
+            for chunks in batches.values():
+                for ps in chunks:
+                    self._update_stacked(ps, kw)
         return loss
+
+    def _update_stacked(self, ps, kw) -> None:
+        """One batched update of same-shape parameters: stacked copies of the
+        parameters, gradients and buffers go through one native call and are copied
+        back (a single parameter is updated in place)."""
+        bufs = [self.state[p]["momentum_buffer"] for p in ps]
+        if len(ps) == 1:
+            muon_update(ps[0], ps[0].grad, bufs[0], **kw)
+            return
+        params = torch.stack([p.detach() for p in ps])
+        grads = torch.stack([p.grad.float() for p in ps])
+        buf = torch.stack(bufs)
+        muon_update(params, grads, buf, **kw)
+        for i, p in enumerate(ps):
+            p.copy_(params[i])
+            bufs[i].copy_(buf[i])

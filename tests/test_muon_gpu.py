@@ -156,3 +156,47 @@ def test_rejects_wrong_dtypes_on_gpu():
     with pytest.raises(RuntimeError, match="float32"):
         torch.ops.muon_ascend950.muon_update(p[None], p[None].bfloat16(), p[None].clone(), 0.9,
                                              True, [1.0, 0.0, 0.0], 0.1, 0.0, 1.0)
+
+
+def test_same_shape_parameters_update_in_one_batched_call(monkeypatch):
+    """Muon (group_shapes, the default) stacks small parameters of one shape into one
+    native call per step: the momentum buffers equal those of one call per parameter
+    bit for bit, the parameters agree to the iteration's precision; a parameter above
+    4M elements and a lone shape stay single calls."""
+    import muon_fusion_ascend950_amd.optim as optim
+    from muon_fusion_ascend950_amd import Muon
+
+    shapes = [(256, 512)] * 3 + [(3, 64, 128)] * 2 + [(200, 36)] * 2 + [(96, 80)] + [(2048, 2049)] * 2
+    gen = torch.Generator().manual_seed(61)
+    base = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    grads = [[torch.randn(s, generator=gen) * 1e-3 for s in shapes] for _ in range(2)]
+    real = optim.muon_update
+    calls = []
+
+    def counting(param, *args, **kwargs):
+        calls.append(tuple(param.shape))
+        return real(param, *args, **kwargs)
+
+    monkeypatch.setattr(optim, "muon_update", counting)
+    results = {}
+    for grouped in (True, False):
+        params = [torch.nn.Parameter(b.clone().to(DEV)) for b in base]
+        opt = Muon(params, lr=0.03, momentum=0.9, weight_decay=0.05, group_shapes=grouped)
+        calls.clear()
+        for step_grads in grads:
+            for p, g in zip(params, step_grads):
+                p.grad = g.to(DEV)
+            opt.step()
+        torch.cuda.synchronize()
+        results[grouped] = ([p.detach().cpu() for p in params],
+                            [opt.state[p]["momentum_buffer"].cpu() for p in params], list(calls))
+    (p_g, b_g, c_g), (p_u, b_u, c_u) = results[True], results[False]
+    assert len(c_u) == 2 * len(shapes)
+    per_step = sorted([(3, 256, 512), (2, 3, 64, 128), (2, 200, 36), (96, 80), (2048, 2049),
+                       (2048, 2049)])
+    assert sorted(c_g) == sorted(per_step * 2)
+    for i, s in enumerate(shapes):
+        assert torch.equal(b_g[i], b_u[i]), f"buffer {s}"
+        moved_g = (p_g[i] - base[i]).double().numpy()
+        moved_u = (p_u[i] - base[i]).double().numpy()
+        assert O.rel_frobenius(moved_g, moved_u) <= 1e-2, s
