@@ -50,3 +50,26 @@ def plan_shape(batch: int, m: int, n: int):
     """The (batch, m, n) the C ABI plans for: M > N with N % 8 != 0 reaches it transposed
     (the reference's wrapper route), every other shape as given."""
     return (batch, n, m) if m > n and n % 8 != 0 else (batch, m, n)
+
+
+# Tuned configurations the sweep also runs (on its first ten M <= N shapes): every tile
+# size, both wave counts, other ring depths, stream-K off and the register-staged family.
+SWEEP_CONFIGS = {
+    "tiles64_depths": {"MUON_POLAR_GRAM_TILE": "64", "MUON_POLAR_POLY_TILE": "64",
+                       "MUON_POLAR_APPLY_TILE_M": "64", "MUON_POLAR_APPLY_TILE_N": "64",
+                       "MUON_POLAR_GRAM_DEPTH": "8", "MUON_POLAR_POLY_DEPTH": "2",
+                       "MUON_POLAR_APPLY_DEPTH": "4", "MUON_POLAR_DIAG_PAIRS": "0"},
+    "tiles128": {"MUON_POLAR_GRAM_TILE": "128", "MUON_POLAR_POLY_TILE": "128",
+                 "MUON_POLAR_APPLY_TILE_M": "128", "MUON_POLAR_APPLY_TILE_N": "128"},
+    "tiles256_4waves": {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_POLY_TILE": "256",
+                        "MUON_POLAR_APPLY_TILE_M": "256", "MUON_POLAR_APPLY_TILE_N": "256",
+                        "MUON_POLAR_WAVES": "4"},
+    "pairs192_unsplit": {"MUON_POLAR_GRAM_TILE": "192", "MUON_POLAR_POLY_TILE": "192",
+                         "MUON_POLAR_STREAM_K": "0"},
+    "register_staged": {"MUON_POLAR_STREAM": "0"},
+}
+
+
+def sweep_config_shapes():
+    """The M <= N shapes the configurations run on."""
+    return [s for s in sweep_shapes() if s[1] <= s[2]][:10]

@@ -17,7 +17,7 @@ from __future__ import annotations
 import pytest
 
 from muon_fusion_ascend950_amd import capi
-from tests.sweep_shapes import plan_shape, sweep_shapes
+from tests.sweep_shapes import SWEEP_CONFIGS, plan_shape, sweep_config_shapes, sweep_shapes
 
 BASELINE_SHAPES = [(4, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (8, 512, 2048),
                    (2, 150, 2050), (1, 129, 130)]
@@ -76,6 +76,16 @@ def test_other_plans_store_inside_their_buffers(shape, occ):
 def test_sweep_plans_store_inside_their_buffers(shape, occ):
     """The shapes of the GPU sweep (tests/test_shape_sweep_gpu.py), checked here first."""
     check(capi.check_plan(*plan_shape(*shape), cus=256, blocks_per_cu=occ))
+
+
+@pytest.mark.parametrize("config", sorted(SWEEP_CONFIGS))
+@pytest.mark.parametrize("shape", sweep_config_shapes())
+def test_sweep_configuration_plans_store_inside_their_buffers(monkeypatch, shape, config):
+    """The tuned configurations of the GPU sweep, checked here first."""
+    for k, v in SWEEP_CONFIGS[config].items():
+        monkeypatch.setenv(k, v)
+    for occ in [(1, 1, 1), (2, 2, 2)]:
+        check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
 
 
 @pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)])

@@ -29,7 +29,9 @@ import pytest
 import torch
 
 from oracle import polar_oracle as O
-from tests.sweep_shapes import sweep_shapes
+import functools
+
+from tests.sweep_shapes import SWEEP_CONFIGS, sweep_config_shapes, sweep_shapes
 from tests.test_polar_step_gpu import bits
 
 pytestmark = pytest.mark.gpu
@@ -69,6 +71,7 @@ def test_sweep_covers_every_width_class_and_orientation():
     assert any(b > 1 for b, _, _ in SHAPES)
 
 
+@functools.lru_cache(maxsize=None)
 def _exact_input(batch, m, n):
     """Sparse ±1 batch whose sums stay exact in fp32, and the oracle's Y for it."""
     wide_shape = (batch, min(m, n), max(m, n))
@@ -89,9 +92,27 @@ def _exact_input(batch, m, n):
 
 @pytest.mark.parametrize("shape", SHAPES, ids=[f"{b}x{m}x{n}" for b, m, n in SHAPES])
 def test_sweep_exact_sums_are_bitwise(shape):
+    _assert_exact_bitwise(shape)
+
+
+CONFIG_SHAPES = sweep_config_shapes()
+
+
+@pytest.mark.parametrize("config", sorted(SWEEP_CONFIGS))
+@pytest.mark.parametrize("shape", CONFIG_SHAPES, ids=[f"{b}x{m}x{n}" for b, m, n in CONFIG_SHAPES])
+def test_sweep_configurations_exact_sums_are_bitwise(monkeypatch, shape, config):
+    """The same exact-sum check with a tuned configuration (tile size, waves, ring
+    depths, stream-K off, register-staged kernels): every kernel family the knobs reach
+    forms the same exact sums."""
+    for k, v in SWEEP_CONFIGS[config].items():
+        monkeypatch.setenv(k, v)
+    _assert_exact_bitwise(shape, config)
+
+
+def _assert_exact_bitwise(shape, config="default"):
     batch, m, n = shape
     x_np, y_ref = _exact_input(batch, m, n)
-    print(f"sweep exact {shape}", flush=True)
+    print(f"sweep exact {shape} {config}", flush=True)
     x = torch.from_numpy(x_np.astype(np.float32)).to(torch.bfloat16).to(DEV)
     y = polar_step(x if batch > 1 else x[0], *EXACT_COEFFS)
     torch.cuda.synchronize()
