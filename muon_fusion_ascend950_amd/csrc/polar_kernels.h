@@ -43,7 +43,10 @@ struct GemmArgs {
     int32_t col_rows, col_k;                 // gram/poly: rows x K of colop; apply: cols x K
     int32_t k_loop;                          // K extent iterated (multiple of 64)
     int32_t out_rows, out_cols;              // store extent (apply only)
-    int32_t out_vec;                         // 1: out rows take 16-byte stores; 0: 2-byte
+    int32_t out_vec;  // 1: out rows take 16-byte stores; 2 (rows of an even number of
+                      // elements from a 4-byte aligned out): 16-byte stores at 4-byte aligned
+                      // addresses for chunks inside the row, 2-byte stores for the chunk
+                      // that ends it; 0: 2-byte stores
                                              // stores (rows of n % 8 != 0 elements)
     int32_t out_cpol;                        // DMA-fed kernels' output stores: 0 plain, 1 nt,
                                              // 2 sc1, 3 nt sc1, 4 sc0 sc1

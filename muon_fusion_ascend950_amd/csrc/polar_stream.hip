@@ -1023,7 +1023,7 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
                 v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
                           hh[6] | (hh[7] << 16)};
             }
-            if (Tr::kSymmetric || g.out_vec) {
+            if (Tr::kSymmetric || g.out_vec == 1 || (g.out_vec == 2 && gc + 8 <= g.out_cols)) {
                 st16(v, gr * g.ld_out + gc);
             } else {
                 // rows of n % 8 != 0 elements: 2-byte stores up to the last column

@@ -541,10 +541,14 @@ def test_ring_depth_rejects_missing_kernel(monkeypatch):
         polar_step(x, *C0)
 
 
-@pytest.mark.parametrize("shape", [(1, 256, 1024), (2, 150, 2050)])
-def test_unaligned_output_pointer(shape):
-    """Y at an address that is not 16-byte aligned (a view one element into a buffer) takes
-    the 2-byte store path of the DMA-fed apply kernel: same bits as an aligned Y."""
+@pytest.mark.parametrize("offset", [1, 2])
+@pytest.mark.parametrize("shape", [(1, 256, 1024), (2, 150, 2050), (1, 129, 130)])
+def test_unaligned_output_pointer(shape, offset):
+    """Y at an address that is not 16-byte aligned (a view `offset` elements into a
+    buffer): at 2 bytes past a 16-byte boundary the DMA-fed apply kernel stores 2 bytes
+    at a time; at 4 bytes past it, rows of an even number of elements take 16-byte stores
+    at 4-byte aligned addresses inside the row and element stores for the chunk that
+    ends it.  Either way the same bits as an aligned Y, and nothing written outside it."""
     from muon_fusion_ascend950_amd import capi
 
     a, b, c = C0
@@ -552,13 +556,14 @@ def test_unaligned_output_pointer(shape):
     ws, _ = capi.alloc_workspace(*shape)
     y = torch.empty_like(x)
     capi.step(x, y, ws, a, b, c)
-    flat = torch.full((x.numel() + 1,), float("nan"), dtype=torch.bfloat16, device=DEV)
-    y_off = flat[1:].view(x.shape)
-    assert y_off.data_ptr() % 16 != 0
+    flat = torch.full((x.numel() + offset + 8,), float("nan"), dtype=torch.bfloat16, device=DEV)
+    y_off = flat[offset:offset + x.numel()].view(x.shape)
+    assert y_off.data_ptr() % 16 == 2 * offset
     capi.step(x, y_off, ws, a, b, c)
     torch.cuda.synchronize()
     assert torch.equal(y, y_off)
-    assert torch.isnan(flat[0])  # nothing written before the view
+    assert torch.isnan(flat[:offset]).all()  # nothing written before the view
+    assert torch.isnan(flat[offset + x.numel():]).all()  # nor after it
 
 
 @pytest.mark.parametrize("shape", [(8, 512, 2048), (1, 1000, 3000), (3, 200, 264), (2, 64, 4096),
