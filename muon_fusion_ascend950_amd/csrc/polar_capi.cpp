@@ -402,12 +402,24 @@ int64_t sk_min_share(int bm, int bn) {
 // tiles: three.
 int64_t sk_max_pieces(int bm, int bn) { return int64_t(bm) * bn <= 64 * 64 ? 4 : 3; }
 
+// Long K over few tiles: where the cut tiles would take at most a quarter of the
+// CUs and a tile's K loop is longer than `pieces` shares of kLongShare K-steps,
+// each tile is cut into up to kLongPieces shares of about kLongShare K-steps (at
+// most one unit per CU).  A 64x64 gram tile of 2048 K-steps ([1,8,131072]) would
+// otherwise run on a few workgroups, or on one (four pieces of one tile round
+// down to no unit at all); the last contributor's partial reads (16 KiB each for
+// 64x64 tiles) cost far less than those K-steps.
+constexpr int64_t kLongShare = 64;
+constexpr int64_t kLongPieces = 32;
+
 SkSplit sk_policy(bool enabled, int64_t tiles, int64_t k_steps, int64_t resident, int64_t cus,
                   int64_t min_share, bool extra_round, int64_t pieces = 3) {
     SkSplit c{tiles, 0, 0, 0};
     if (!enabled || resident < 8) return c;
     const int64_t rem = tiles % resident;
     if (rem == 0 || rem * 4 > resident * 3 || rem * 4 > cus * 3) return c;
+    if (k_steps > pieces * kLongShare && rem * pieces * 4 <= cus)
+        pieces = std::max(pieces, std::min({kLongPieces, k_steps / kLongShare, cus / rem}));
     int64_t units = std::min<int64_t>(resident, rem * pieces);
     // pieces beyond three stop at one unit per CU
     if (units > cus && rem * 3 <= cus) units = cus;

@@ -22,7 +22,8 @@ from tests.sweep_shapes import SWEEP_CONFIGS, plan_shape, sweep_config_shapes, s
 BASELINE_SHAPES = [(4, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (8, 512, 2048),
                    (2, 150, 2050), (1, 129, 130)]
 MORE_SHAPES = [(3, 1024, 4096), (16, 256, 1024), (1, 1000, 3000), (2, 700, 1800), (1, 3000, 1000),
-               (1, 8192, 16384), (2, 6144, 8192), (4000, 16, 40), (1, 64, 100000), (1, 2048, 520)]
+               (1, 8192, 16384), (2, 6144, 8192), (4000, 16, 40), (1, 64, 100000), (1, 2048, 520),
+               (1, 8, 131072), (1, 65536, 8), (2, 3, 40000), (1, 128, 65536)]
 OCCUPANCIES = [(1, 1, 1), (2, 2, 2), (1, 2, 2), (2, 1, 1), (3, 3, 3), (4, 4, 4)]
 
 
@@ -86,6 +87,19 @@ def test_sweep_configuration_plans_store_inside_their_buffers(monkeypatch, shape
         monkeypatch.setenv(k, v)
     for occ in [(1, 1, 1), (2, 2, 2)]:
         check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
+
+
+@pytest.mark.parametrize("shape,units", [((1, 8, 131072), 32), ((1, 64, 100000), 24),
+                                         ((1, 65536, 8), 16), ((1, 128, 65536), 48)])
+def test_long_k_over_few_tiles_is_cut_into_many_shares(shape, units):
+    """A gram stage of a few 64x64 tiles with a long K loop is cut into shares of about
+    64 K-steps (up to 32 per tile), where the default pieces (at most four per tile)
+    would leave it to a few workgroups or, for one tile, to one."""
+    plan = capi.check_plan(*shape, cus=256, blocks_per_cu=(1, 1, 1))
+    check(plan)
+    gram = plan.stage[0]
+    assert gram.tile_m == 64 and gram.dp_tiles == 0 and gram.sk_units == units
+    assert gram.k_steps * gram.total_tiles / gram.sk_units >= 60  # shares of about 64 K-steps
 
 
 @pytest.mark.parametrize("shape", [(1, 4096, 14336), (1, 14336, 4096)])

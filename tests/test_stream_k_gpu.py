@@ -34,7 +34,10 @@ EXACT_COEFFS = (2.0, -1.0, 1.0)
 # apply's last round runs as 256x128 halves, test_halves_gpu.py; it is split here
 # with 256x256 triangular tiles, and with the halves off.  [2,4096,4096] takes the
 # two-round split of gram and poly: 256 units of 68 K-steps over all 272 tiles;
-# [4096,17408] that of apply: 768 whole tiles, then 256 units over the last 320.)
+# [4096,17408] that of apply: 768 whole tiles, then 256 units over the last 320.
+# [1,64,100000] and [1,8,131072]: one 64x64 gram tile of 1563 / 2048 K-steps cut
+# into 24 / 32 shares of about 64 K-steps, so the last contributor adds 23 / 31
+# partials.)
 SPLIT_SHAPES = [(2, 512, 4096), (2, 1536, 4096), (1, 700, 5000), (2, 1500, 3000)]
 # 256x256 tiles for the triangular stages (256 KiB partials)
 BIG_TILES = {"MUON_POLAR_GRAM_TILE": "256", "MUON_POLAR_POLY_TILE": "256"}
@@ -83,7 +86,7 @@ def test_split_is_in_use(shape):
 @pytest.mark.parametrize("shape,env", [(s, {}) for s in SPLIT_SHAPES] +
                          [((1, 4096, 14336), HEADLINE_SPLIT), ((2, 2048, 4096), BIG_TILES),
                           ((1, 4096, 14336), BIG_TILES), ((2, 4096, 4096), {}),
-                          ((1, 4096, 17408), {})])
+                          ((1, 4096, 17408), {}), ((1, 64, 100000), {}), ((1, 8, 131072), {})])
 def test_exact_sums_are_bitwise(monkeypatch, shape, env, split):
     monkeypatch.setenv("MUON_POLAR_STREAM_K", split)
     for k, v in env.items():
