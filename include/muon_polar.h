@@ -43,7 +43,11 @@
  * Otherwise (odd n, or X not 4-byte aligned) each step first copies X into a
  * zero-padded [batch, m, roundup(n, 64)] buffer at the end of the workspace, which
  * info.workspace_bytes includes for every n % 8 != 0.  Y is written at its own
- * width (2-byte stores when n % 8 != 0).  Shapes whose padded copy would reach
+ * width: 16-byte stores when n % 8 == 0 and y is 16-byte aligned; otherwise, with a
+ * 4-byte aligned y, 16-byte stores for the 8-element chunks inside each row that starts
+ * on a 4-byte boundary (every row for even n, every other row for odd n) and 2-byte
+ * stores for the rest; 2-byte stores throughout when y is only 2-byte aligned.
+ * Shapes whose padded copy would reach
  * 2^30 elements per matrix are rejected ("matrix too large"), like X itself.
  *
  * Buffers: x, y and the workspace must be pairwise disjoint (no in-place call:

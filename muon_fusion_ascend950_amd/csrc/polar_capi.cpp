@@ -876,11 +876,11 @@ StageLaunch apply_launch(const Plan &p, const void *poly, const void *x, int64_t
     g.s_acc = 1.0f;
     L.extent[0] = p.mp * p.mp * 2;
     L.extent[1] = L.extent[2] = m * ldx * 2;
-    g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : (n % 2 == 0 && aligned4(y)) ? 2 : 0;
+    g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : !aligned4(y) ? 0 : n % 2 == 0 ? 2 : 3;
     g.group_n = apply_group(p);
     g.out_cpol = p.y_cpol;
     // DMA-fed kernel: X rows of whole 16-byte chunks (Y any alignment: 16-byte stores
-    // for out_vec 1, and for 2 inside the rows; 2-byte stores otherwise);
+    // for out_vec 1, and for 2 and 3 inside the rows they cover; 2-byte stores otherwise);
     // register-staged kernel: vectors on both or neither.
     const bool xvec = (ldx % 8 == 0) && aligned16(x);
     L.stage = Stage::Apply;
@@ -1185,8 +1185,8 @@ void stage_extent(const StageLaunch &L, bool splits, muon_polar_stage_extent &e)
             const int last_row = std::min(row0 + L.bm, g.out_rows) - 1;
             if (last_row < row0 || col0 >= g.out_cols) return;
             // last 16-byte chunk that starts inside the matrix; 8-element vector
-            // stores when out_vec is 1, else (2: vectors only inside the row) stores
-            // up to the last column
+            // stores when out_vec is 1, else (2 and 3: vectors only inside the row)
+            // stores up to the last column
             const int last_chunk = col0 + 8 * ((std::min(col0 + bn, g.out_cols) - 1 - col0) / 8);
             const int64_t end_col =
                 g.out_vec == 1 ? last_chunk + 8 : std::min(col0 + bn, g.out_cols);

@@ -46,7 +46,9 @@ struct GemmArgs {
     int32_t out_vec;  // 1: out rows take 16-byte stores; 2 (rows of an even number of
                       // elements from a 4-byte aligned out): 16-byte stores at 4-byte aligned
                       // addresses for chunks inside the row, 2-byte stores for the chunk
-                      // that ends it; 0: 2-byte stores
+                      // that ends it; 3 (an odd number of elements, 4-byte aligned out): as
+                      // 2 on the rows that start on a 4-byte boundary (even element offset),
+                      // 2-byte stores on the others; 0: 2-byte stores
                                              // stores (rows of n % 8 != 0 elements)
     int32_t out_cpol;                        // DMA-fed kernels' output stores: 0 plain, 1 nt,
                                              // 2 sc1, 3 nt sc1, 4 sc0 sc1

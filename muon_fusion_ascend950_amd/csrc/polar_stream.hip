@@ -1002,7 +1002,11 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
             // diagonal pairs: tile ot of the two at (row0 + ot * BM, row0 + ot * BM)
             const int ot = DG ? idx / (BM * kChunksPerRow) : 0;
             const int ti = DG ? idx - ot * (BM * kChunksPerRow) : idx;
-            const int row = ti / kChunksPerRow, c = ti % kChunksPerRow;
+            int row = ti / kChunksPerRow;
+            const int c = ti % kChunksPerRow;
+            // out_vec 3: even rows first, then odd ones, so that the rows a wave stores
+            // share one parity and so one store path (row0 is even)
+            if (!Tr::kSymmetric && g.out_vec == 3) row = row < BM / 2 ? 2 * row : 2 * row - (BM - 1);
             const int sr0 = DG ? row0 + ot * BM : row0, sc0 = DG ? sr0 : col0;
             const int gr = sr0 + row, gc = sc0 + 8 * c;
             if constexpr (!Tr::kSymmetric) {
@@ -1023,7 +1027,11 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
                 v = u32x4{hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
                           hh[6] | (hh[7] << 16)};
             }
-            if (Tr::kSymmetric || g.out_vec == 1 || (g.out_vec == 2 && gc + 8 <= g.out_cols)) {
+            // out_vec 3: a row starts on a 4-byte boundary when its element offset from
+            // the (4-byte aligned) out is even
+            const bool vec_row =
+                g.out_vec == 2 || (g.out_vec == 3 && ((bt * g.sb_out + int64_t(gr) * g.ld_out) & 1) == 0);
+            if (Tr::kSymmetric || g.out_vec == 1 || (vec_row && gc + 8 <= g.out_cols)) {
                 st16(v, gr * g.ld_out + gc);
             } else {
                 // rows of n % 8 != 0 elements: 2-byte stores up to the last column

@@ -542,13 +542,17 @@ def test_ring_depth_rejects_missing_kernel(monkeypatch):
 
 
 @pytest.mark.parametrize("offset", [1, 2])
-@pytest.mark.parametrize("shape", [(1, 256, 1024), (2, 150, 2050), (1, 129, 130)])
+@pytest.mark.parametrize("shape", [(1, 256, 1024), (2, 150, 2050), (1, 129, 130), (3, 129, 257),
+                                   (2, 200, 1001)])
 def test_unaligned_output_pointer(shape, offset):
     """Y at an address that is not 16-byte aligned (a view `offset` elements into a
     buffer): at 2 bytes past a 16-byte boundary the DMA-fed apply kernel stores 2 bytes
     at a time; at 4 bytes past it, rows of an even number of elements take 16-byte stores
     at 4-byte aligned addresses inside the row and element stores for the chunk that
-    ends it.  Either way the same bits as an aligned Y, and nothing written outside it."""
+    ends it, and rows of an odd number do so on the rows whose start is 4-byte aligned
+    (every other row; with an odd row count the pattern flips from one matrix of the
+    batch to the next).  Either way the same bits as an aligned Y, and nothing written
+    outside it."""
     from muon_fusion_ascend950_amd import capi
 
     a, b, c = C0
