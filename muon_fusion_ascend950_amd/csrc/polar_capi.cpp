@@ -626,7 +626,7 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
     p.express_norm_offset = p.express_x_offset + align256(size_t(batch) * m * n * 2u);
     p.express_workspace_bytes =
         p.express_norm_offset +
-        align256(size_t(batch) * muon_polar::norm_chunks(m * n) * sizeof(float));
+        align256(size_t(batch) * muon_polar::norm_chunks(batch, m * n) * sizeof(float));
     p.muon_o_offset = p.express_workspace_bytes;
     p.muon_workspace_bytes = p.muon_o_offset + align256(size_t(batch) * m * n * 2u);
     out = p;

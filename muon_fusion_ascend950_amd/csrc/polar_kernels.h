@@ -125,9 +125,11 @@ int stream_blocks_per_cu(Stage s, int bm, int bn, int waves, int depth);
 
 // Per-matrix normalisation y = x / (‖x‖_F·1.01 + 1e-6) of `batch` matrices of mn
 // elements (reference recipe rounding points; polar_norm.hip).  `partial` holds
-// batch * norm_chunks(mn) floats; vec: mn % 8 == 0 and 16-byte aligned x and y.
-constexpr int64_t kNormChunk = 256 * 8 * 32;  // elements per partial sum
-int64_t norm_chunks(int64_t mn);
+// batch * norm_chunks(batch, mn) floats; vec: mn % 8 == 0 and 16-byte aligned x and y.
+// Elements per partial sum (a power of two from 4096 to 2^20) and partial sums per
+// matrix for `batch` matrices of mn elements.
+int64_t norm_chunk(int64_t batch, int64_t mn);
+int64_t norm_chunks(int64_t batch, int64_t mn);
 hipError_t launch_normalize(const uint16_t *x, uint16_t *y, float *partial, int64_t batch,
                             int64_t mn, bool vec, hipStream_t stream);
 // The scale pass alone, from partial sums already in `partial`.
