@@ -61,7 +61,10 @@ def test_steps_equal_chained_polar_step(shape, k):
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("shape", [(3, 40, 70), (2, 150, 2050), (8, 512, 2048), (1, 4096, 14336)])
+# partial sums over chunks of 4096 elements (ragged: [5,1000,1001], odd m·n), 8192 with a
+# 16-element last chunk ([4100,4100]) and 16384 ([4096,14336])
+@pytest.mark.parametrize("shape", [(3, 40, 70), (2, 150, 2050), (8, 512, 2048), (5, 1000, 1001),
+                                   (1, 4100, 4100), (1, 4096, 14336)])
 def test_normalization(shape):
     x = raw_input(shape, seed=41)
     x[0] *= 8.0  # matrices of a batch get different scales
