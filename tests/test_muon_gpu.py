@@ -46,6 +46,9 @@ def f32_bits(a) -> np.ndarray:
 
 
 def assert_f32_equal(got, want, what):
+    # both sides of a comparison can come from the GPU (O from polar_express): equal
+    # NaNs would pass a bit comparison, so the values must be finite too
+    assert np.isfinite(f32_bits(want).view(np.float32)).all(), f"{what}: non-finite values"
     gb, wb = f32_bits(got).ravel(), f32_bits(want).ravel()
     bad = np.flatnonzero(gb != wb)
     assert bad.size == 0, f"{what}: {bad.size} of {gb.size} differ, first at {bad[0]}"
