@@ -114,6 +114,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_scale_kernel(const uint16_t
     const int64_t e0 = int64_t(c) * chunk;
     const int64_t e1 = e0 + chunk < mn ? e0 + chunk : mn;
     if (vec) {
+        const __amdgpu_buffer_rsrc_t rs_y = store_rsrc(yb + e0);
         for (int64_t e = e0 + threadIdx.x * 8; e < e1; e += kNormUnroll * kNormStride) {
             u32x4 v[kNormUnroll];
 #pragma unroll
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_scale_kernel(const uint16_t
                     const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(v[u][w] >> 16) / d);
                     o[w] = lo | (hi << 16);
                 }
-                store16_sc1(yb + e + u * kNormStride, o);
+                store16_sc1(rs_y, static_cast<uint32_t>((e + u * kNormStride - e0) * 2), o);
             }
         }
     } else {
@@ -175,6 +176,7 @@ __global__ __launch_bounds__(kNormThreads) void muon_momentum_kernel(
     };
     if (kOrder8) {
         constexpr int kU = kVec ? kMomentumUnroll : 1;
+        const __amdgpu_buffer_rsrc_t rs_x0 = store_rsrc(x0 + base + e0);
         for (int64_t e = e0 + threadIdx.x * 8; e < e1; e += kU * kNormStride) {
             float gv[kU][8], bv[kU][8];
 #pragma unroll
@@ -211,7 +213,7 @@ __global__ __launch_bounds__(kNormThreads) void muon_momentum_kernel(
                     *reinterpret_cast<f32x4 *>(buf + base + eu) = f32x4{nb[0], nb[1], nb[2], nb[3]};
                     *reinterpret_cast<f32x4 *>(buf + base + eu + 4) =
                         f32x4{nb[4], nb[5], nb[6], nb[7]};
-                    store16_sc1(x0 + base + eu,
+                    store16_sc1(rs_x0, static_cast<uint32_t>((eu - e0) * 2),
                                 u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16),
                                       h[4] | (h[5] << 16), h[6] | (h[7] << 16)});
                 } else {
@@ -289,7 +291,10 @@ __global__ __launch_bounds__(kNormThreads) void pad_rows_kernel(const uint16_t *
     // row_chunks = np / 8: chunks per padded row; vec: 16-byte loads of whole
     // chunks (n % 8 == 0 and x 16-byte aligned)
     const int64_t stride = int64_t(gridDim.x) * kNormThreads;
-    for (int64_t q = int64_t(blockIdx.x) * kNormThreads + threadIdx.x; q < chunks; q += stride) {
+    for (int64_t q0 = int64_t(blockIdx.x) * kNormThreads; q0 < chunks; q0 += stride) {
+        const int64_t q = q0 + threadIdx.x;
+        if (q >= chunks) break;
+        const __amdgpu_buffer_rsrc_t rs = store_rsrc(xp + q0 * 8);  // this block's chunks
         const int64_t r = q / row_chunks;
         const int c0 = static_cast<int>(q - r * row_chunks) * 8;
         const uint16_t *src = x + r * n + c0;
@@ -303,7 +308,7 @@ __global__ __launch_bounds__(kNormThreads) void pad_rows_kernel(const uint16_t *
             v = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
                       h[6] | (h[7] << 16)};
         }
-        store16_sc1(xp + q * 8, v);
+        store16_sc1(rs, static_cast<uint32_t>(threadIdx.x) * 16u, v);
     }
 }
 

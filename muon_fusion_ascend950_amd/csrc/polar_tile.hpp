@@ -235,9 +235,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // Issued as inline assembly so the compiler neither reorders LDS traffic around
 // it nor inserts its own waits (the LDS-DMA builtin makes it wait for the transfer
 // before every later LDS read); the kernels wait with vmcnt explicitly.  The LDS
-// address is an M0 input operand, which the compiler loads itself.
+// address is an M0 input operand, which the compiler loads itself, often with the
+// instruction right before the asm.  On gfx9 an LDS DMA needs one wait state after
+// a scalar write of M0; the compiler's hazard check cannot see inside the asm (for
+// the LDS-DMA builtin it inserts that s_nop itself), so the asm carries it.  (A
+// VALU write of an SGPR that a memory instruction reads needs five wait states; the
+// descriptors are built well before their DMAs, none closer in the assembly of
+// this build.)
 __device__ __forceinline__ void dma_16B(i32x4 rsrc, uint32_t lds_base, uint32_t voffset) {
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                  :
                  : "v"(voffset), "s"(rsrc), "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
                  : "memory");
@@ -254,9 +260,17 @@ __device__ __forceinline__ void wait_vm_barrier() {
 
 // 16-byte store at device scope (sc1): written through the XCD's L2, so the line is
 // not dirty there when the kernel ends, and a kernel on another XCD reads the data
-// from the memory side.  For buffers the next kernel of a step reads.
-__device__ __forceinline__ void store16_sc1(void *p, u32x4 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+// from the memory side.  For buffers the next kernel of a step reads.  `rs` covers
+// 2^31 bytes from a workgroup-uniform base (store_rsrc) and `off` is the byte offset
+// from it.  The store is the compiler's buffer-store builtin, not inline assembly:
+// a 16-byte store reads its data registers after it issues, and only for an
+// instruction it can see does the compiler insert the wait states that keep the
+// next VALU write of those registers from changing the stored data.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t store_rsrc(void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void store16_sc1(__amdgpu_buffer_rsrc_t rs, uint32_t off, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 16);
 }
 
 template <int N>
