@@ -1028,9 +1028,11 @@ __device__ __forceinline__ void stream_segment(const GemmArgs &g, uint16_t *smem
                           hh[6] | (hh[7] << 16)};
             }
             // out_vec 3: a row starts on a 4-byte boundary when its element offset from
-            // the (4-byte aligned) out is even
+            // the (4-byte aligned) out, bt * sb_out + gr * ld_out, is even (parities of the
+            // products and the sum from the low bits)
             const bool vec_row =
-                g.out_vec == 2 || (g.out_vec == 3 && ((bt * g.sb_out + int64_t(gr) * g.ld_out) & 1) == 0);
+                g.out_vec == 2 ||
+                (g.out_vec == 3 && (((bt & g.sb_out) ^ (gr & g.ld_out)) & 1) == 0);
             if (Tr::kSymmetric || g.out_vec == 1 || (vec_row && gc + 8 <= g.out_cols)) {
                 st16(v, gr * g.ld_out + gc);
             } else {
