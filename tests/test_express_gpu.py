@@ -48,8 +48,11 @@ def raw_input(shape, seed, scale=3.0):
     return (torch.randn(shape, dtype=torch.bfloat16, generator=gen) * scale).to(DEV)
 
 
+# widths: multiples of 64 and of 8, even, odd (padded copy of X in every step; Y rows of
+# alternating alignment, [3,129,257]); tall: right-Gram form ([2,1000,136]) and the
+# transposed route of an unaligned width ([1,515,130])
 @pytest.mark.parametrize("shape", [(8, 512, 2048), (2, 150, 2050), (3, 1024, 8192), (1, 4096, 14336),
-                                   (2, 300, 1000)])
+                                   (2, 300, 1000), (3, 129, 257), (2, 1000, 136), (1, 515, 130)])
 @pytest.mark.parametrize("k", [1, 2, 5])
 def test_steps_equal_chained_polar_step(shape, k):
     x = O.make_input(shape, seed=40).to(DEV)

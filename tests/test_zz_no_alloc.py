@@ -34,10 +34,13 @@ def with_workspace(capi, x, coeffs):
 
 
 def test_noalloc_equals_workspace_entry(capi):
-    # [4096,14336]: every stage cuts its last round (partials and arrival words in
-    # the scratch); then smaller shapes over the scratch that call left behind
+    # [4096,14336] first (the largest A and P in the scratch), then smaller shapes over
+    # what that call left behind: [2,150,2050] cuts its gram tiles by stream-K
+    # (partials and arrival words in the scratch), [3,129,257] takes the padded copy of
+    # X (also in the scratch), [2,1000,136] the right-Gram form
     for shape, seed in (((1, 4096, 14336), 0), ((8, 512, 2048), 1), ((2, 150, 2050), 2),
-                        ((1, 129, 130), 3), ((2, 300, 1000), 4)):
+                        ((1, 129, 130), 3), ((2, 300, 1000), 4), ((3, 129, 257), 5),
+                        ((2, 1000, 136), 6)):
         print(f"noalloc {shape}", flush=True)
         x = O.make_input(shape, seed=seed).to(DEV)
         coeffs = O.COEFFICIENTS[seed % 5]
