@@ -27,9 +27,11 @@ DEV = "cuda"
 # wide, batch, tall with N % 8 == 0 (right-Gram), ragged (scalar element paths), tall
 # with N % 8 != 0 (transposed route), headline parameter shape
 # partial sums of squares over chunks of 4096 elements (the small shapes), 8192 with a
-# 16-element last chunk ([4100,4100]) and 16384 ([4096,14336])
+# 16-element last chunk ([4100,4100]) and 16384 ([4096,14336]); m·n not a multiple of 8
+# ([3,150,2050], [2,129,257]: the momentum pass's element-wise path); odd width
+# ([2,129,257]: the padded copy of X in every step)
 SHAPES = [(1, 512, 2048), (2, 300, 1000), (1, 2048, 512), (3, 150, 2050), (1, 520, 130),
-          (1, 4100, 4100), (1, 4096, 14336)]
+          (2, 129, 257), (1, 4100, 4100), (1, 4096, 14336)]
 
 
 @pytest.fixture(scope="module", autouse=True)
