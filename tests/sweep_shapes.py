@@ -73,3 +73,49 @@ SWEEP_CONFIGS = {
 def sweep_config_shapes():
     """The M <= N shapes the configurations run on."""
     return [s for s in sweep_shapes() if s[1] <= s[2]][:10]
+
+
+# Configurations of the random-case sweep: the tuned ones above, the defaults, and the
+# default with one of its plan features off (the two-round stream-K split, diagonal
+# pairs, apply's column halves).
+FUZZ_CONFIGS = dict(SWEEP_CONFIGS)
+FUZZ_CONFIGS.update({
+    "default": {},
+    "one_round": {"MUON_POLAR_SK_ROUNDS": "0"},
+    "no_pairs": {"MUON_POLAR_DIAG_PAIRS": "0"},
+    "no_halves": {"MUON_POLAR_APPLY_HALVES": "0"},
+})
+
+
+def fuzz_cases(count: int = 160, seed: int = 777):
+    """Seeded random (shape, configuration, Y offset in elements) cases: batch 1-4,
+    sides up to about 4500 (at most 6M elements), all four width classes, 30% tall;
+    Y at 0, 1 or 2 elements past a 16-byte boundary (only 0 for the right-Gram form,
+    which needs a 16-byte aligned Y)."""
+    rng = np.random.default_rng(seed)
+    names = sorted(FUZZ_CONFIGS)
+    cases = []
+    while len(cases) < count:
+        batch = int(rng.choice([1, 1, 2, 3, 4]))
+        short = int(rng.integers(1, 1500))
+        long_ = short + int(rng.integers(0, 3000))
+        kind = int(rng.integers(0, 4))
+        if kind == 0:
+            long_ |= 1
+        elif kind == 1:
+            long_ = max(2, long_ - long_ % 8 + int(rng.choice([2, 4, 6])))
+        elif kind == 2:
+            long_ = max(8, long_ - long_ % 8)
+        else:
+            long_ = max(64, long_ - long_ % 64)
+        long_ = max(long_, short)
+        tall = rng.random() < 0.3 and short < long_
+        m, n = (long_, short) if tall else (short, long_)
+        config = names[int(rng.integers(0, len(names)))]
+        offset = int(rng.choice([0, 0, 1, 2]))
+        if batch * m * n > 6_000_000:
+            continue
+        if m > n:
+            offset = 0
+        cases.append(((batch, m, n), config, offset))
+    return cases

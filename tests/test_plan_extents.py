@@ -17,7 +17,8 @@ from __future__ import annotations
 import pytest
 
 from muon_fusion_ascend950_amd import capi
-from tests.sweep_shapes import SWEEP_CONFIGS, plan_shape, sweep_config_shapes, sweep_shapes
+from tests.sweep_shapes import (FUZZ_CONFIGS, SWEEP_CONFIGS, fuzz_cases, plan_shape,
+                                 sweep_config_shapes, sweep_shapes)
 
 BASELINE_SHAPES = [(4, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (8, 512, 2048),
                    (2, 150, 2050), (1, 129, 130)]
@@ -87,6 +88,18 @@ def test_sweep_configuration_plans_store_inside_their_buffers(monkeypatch, shape
         monkeypatch.setenv(k, v)
     for occ in [(1, 1, 1), (2, 2, 2)]:
         check(capi.check_plan(*shape, cus=256, blocks_per_cu=occ))
+
+
+def test_random_case_plans_store_inside_their_buffers(monkeypatch):
+    """Every case of the GPU's random-case sweep, under its configuration, at every
+    occupancy, checked here first."""
+    for shape, config, _offset in fuzz_cases():
+        for k in {k for v in FUZZ_CONFIGS.values() for k in v}:
+            monkeypatch.delenv(k, raising=False)
+        for k, v in FUZZ_CONFIGS[config].items():
+            monkeypatch.setenv(k, v)
+        for occ in OCCUPANCIES:
+            check(capi.check_plan(*plan_shape(*shape), cus=256, blocks_per_cu=occ))
 
 
 @pytest.mark.parametrize("shape,units", [((1, 8, 131072), 32), ((1, 64, 100000), 24),
