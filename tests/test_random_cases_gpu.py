@@ -10,6 +10,8 @@ Every case's plan was checked on the CPU first
 (``tests/test_plan_extents.py::test_random_case_plans_store_inside_their_buffers``).
 With sparse ±1 X and integer coefficients every sum is exact in fp32, so Y must equal
 the oracle's rounding-point emulation bit for bit, and nothing may be written outside Y.
+The first 40 cases also run polar_express (1-5 steps, one workspace reused across the
+steps) against as many chained polar_step calls, bit for bit.
 """
 
 from __future__ import annotations
@@ -79,3 +81,31 @@ def test_random_case_is_bitwise(monkeypatch, case):
                            f"{np.unravel_index(bad[0], got.shape)}")
     if flat is not None:
         assert torch.isnan(flat[:offset]).all() and torch.isnan(flat[offset + x.numel():]).all()
+
+
+EXPRESS_CASES = CASES[:40]
+
+
+@pytest.mark.parametrize("case", range(len(EXPRESS_CASES)),
+                         ids=[f"{b}x{m}x{n}-{c}" for (b, m, n), c, _ in EXPRESS_CASES])
+def test_random_case_express_equals_chained_steps(monkeypatch, case):
+    """polar_express without normalisation (one plan and one workspace reused across the
+    steps, the iterate alternating between two buffers) equals chained polar_step calls
+    (a fresh workspace each) bit for bit, for 1 to 5 steps, under the case's configuration."""
+    import muon_fusion_ascend950_amd as mf
+
+    (batch, m, n), config, _offset = EXPRESS_CASES[case]
+    for k in KNOBS:
+        monkeypatch.delenv(k, raising=False)
+    for k, v in FUZZ_CONFIGS[config].items():
+        monkeypatch.setenv(k, v)
+    steps = 1 + case % 5
+    print(f"random express case {case}: {(batch, m, n)} {config} steps {steps}", flush=True)
+    x = O.make_input((batch, m, n), seed=2000 + case).to(DEV)
+    got = mf.polar_express(x, O.COEFFICIENTS[:steps], normalize=False)
+    want = x
+    for a, b, c in O.COEFFICIENTS[:steps]:
+        want = mf.polar_step(want, a, b, c)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, want)
