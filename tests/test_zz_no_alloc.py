@@ -56,6 +56,34 @@ def test_noalloc_equals_workspace_entry(capi):
     assert torch.equal(y2, want)
 
 
+def test_noalloc_random_cases_equal_workspace_entry(capi, monkeypatch):
+    """Forty of the seeded random cases (tests/sweep_shapes.py fuzz_cases) in a row on
+    the one scratch, each under its configuration: every call finds the previous call's
+    A, P, partials and arrival words there, of another shape and plan."""
+    from tests.sweep_shapes import FUZZ_CONFIGS, fuzz_cases
+
+    knobs = sorted({k for v in FUZZ_CONFIGS.values() for k in v})
+    # the cases the C ABI takes as given (the reference wrapper transposes M > N with
+    # N % 8 != 0 outside it)
+    cases = [c for c in fuzz_cases() if not (c[0][1] > c[0][2] and c[0][2] % 8 != 0)][:40]
+    ran = 0
+    for i, ((batch, m, n), config, _offset) in enumerate(cases):
+        for k in knobs:
+            monkeypatch.delenv(k, raising=False)
+        for k, v in FUZZ_CONFIGS[config].items():
+            monkeypatch.setenv(k, v)
+        print(f"noalloc random case {i}: {(batch, m, n)} {config}", flush=True)
+        x = O.make_input((batch, m, n), seed=3000 + i).to(DEV)
+        coeffs = O.COEFFICIENTS[i % 5]
+        y = torch.empty_like(x)
+        capi.step_noalloc(x, y, *coeffs)
+        want = with_workspace(capi, x, coeffs)
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), (i, (batch, m, n), config)
+        ran += 1
+    assert ran == 40
+
+
 def test_noalloc_right_gram_form(capi):
     x = O.make_input((1, 2048, 512), seed=4).to(DEV)
     y = torch.empty_like(x)
