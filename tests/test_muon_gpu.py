@@ -88,6 +88,43 @@ def test_update_chain_is_bitwise(shape, nesterov, wd):
     assert_f32_equal(p_d, want_p, "param")
 
 
+def _random_muon_cases():
+    from tests.sweep_shapes import fuzz_cases
+
+    return [c for c in fuzz_cases()[40:70]]
+
+
+@pytest.mark.parametrize("case", _random_muon_cases(),
+                         ids=[f"{b}x{m}x{n}-{c}" for (b, m, n), c, _ in _random_muon_cases()])
+def test_random_case_update_chain_is_bitwise(monkeypatch, case):
+    """Thirty of the seeded random cases (tests/sweep_shapes.py fuzz_cases), each under
+    its configuration: the momentum buffer bit-exact against the oracle, the parameter
+    bit-exact against the oracle's parameter pass over polar_express of the oracle's bf16
+    input."""
+    from muon_fusion_ascend950_amd import muon_update, polar_express
+    from muon_fusion_ascend950_amd.optim import default_lr_scale
+    from tests.sweep_shapes import FUZZ_CONFIGS
+
+    shape, config, _offset = case
+    for k in {k for v in FUZZ_CONFIGS.values() for k in v}:
+        monkeypatch.delenv(k, raising=False)
+    for k, v in FUZZ_CONFIGS[config].items():
+        monkeypatch.setenv(k, v)
+    print(f"muon random case {shape} {config}", flush=True)
+    p, g, buf = state(shape, seed=53)
+    lr, beta = 0.05, 0.9
+    p_d, g_d, buf_d = p.to(DEV), g.to(DEV), buf.to(DEV)
+    muon_update(p_d, g_d, buf_d, lr=lr, momentum=beta, nesterov=True, weight_decay=0.01)
+    torch.cuda.synchronize()
+    new_buf, u = O.muon_momentum(g.numpy(), buf.numpy(), beta, True)
+    assert_f32_equal(buf_d, new_buf, "momentum buffer")
+    o = polar_express(torch.from_numpy(u).to(torch.bfloat16).to(DEV))
+    torch.cuda.synchronize()
+    scale = default_lr_scale(shape[-2], shape[-1])
+    want_p = O.muon_param_update(p.numpy(), o.float().cpu().numpy(), lr, 0.01, scale)
+    assert_f32_equal(p_d, want_p, "param")
+
+
 @pytest.mark.parametrize("shape", [(2, 300, 1000), (1, 2048, 512), (1, 520, 130)])
 def test_direction_matches_oracle(shape):
     """O from the parameter change against the oracle's whole update (float64 sums,
