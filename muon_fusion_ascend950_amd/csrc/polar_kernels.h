@@ -49,8 +49,7 @@ struct GemmArgs {
                       // that ends it; 3 (an odd number of elements, 4-byte aligned out): as
                       // 2 on the rows that start on a 4-byte boundary (even element offset),
                       // 2-byte stores on the others; 0: 2-byte stores
-                                             // stores (rows of n % 8 != 0 elements)
-    int32_t out_cpol;                        // DMA-fed kernels' output stores: 0 plain, 1 nt,
+    int32_t out_cpol;                       // DMA-fed kernels' output stores: 0 plain, 1 nt,
                                              // 2 sc1, 3 nt sc1, 4 sc0 sc1
     int32_t tiles_m, tiles_n, tiles_per_batch;
     float s_epi, s_acc;  // poly: b, c;  apply: a, 1
