@@ -11,7 +11,8 @@ Every case's plan was checked on the CPU first
 With sparse ±1 X and integer coefficients every sum is exact in fp32, so Y must equal
 the oracle's rounding-point emulation bit for bit, and nothing may be written outside Y.
 The first 40 cases also run polar_express (1-5 steps, one workspace reused across the
-steps) against as many chained polar_step calls, bit for bit.
+steps) against as many chained polar_step calls, bit for bit, and 30 wide cases run the
+stage entry points (gram, poly, apply) against the step and the oracle.
 """
 
 from __future__ import annotations
@@ -109,3 +110,53 @@ def test_random_case_express_equals_chained_steps(monkeypatch, case):
     torch.cuda.synchronize()
     assert torch.isfinite(got.float()).all()
     assert torch.equal(got, want)
+
+
+STAGE_CASES = [c for c in CASES if c[0][1] <= c[0][2]][:30]
+
+
+@pytest.mark.parametrize("case", range(len(STAGE_CASES)),
+                         ids=[f"{b}x{m}x{n}-{c}" for (b, m, n), c, _ in STAGE_CASES])
+def test_random_case_stage_calls(monkeypatch, case):
+    """The stage entry points (gram, poly, apply) on random cases (M <= N), each under its
+    configuration: given the step's workspace they reproduce the step's A, P and Y bit for
+    bit on a random input; without a workspace (one tile per workgroup, no split) their Y
+    equals the oracle's bit for bit on the exact-sum input."""
+    from muon_fusion_ascend950_amd import capi
+
+    (batch, m, n), config, _offset = STAGE_CASES[case]
+    for k in KNOBS:
+        monkeypatch.delenv(k, raising=False)
+    for k, v in FUZZ_CONFIGS[config].items():
+        monkeypatch.setenv(k, v)
+    print(f"random stage case {case}: {(batch, m, n)} {config}", flush=True)
+    a, b, c = O.COEFFICIENTS[case % 5]
+    x = O.make_input((batch, m, n), seed=4000 + case).to(DEV)
+    ws, info = capi.alloc_workspace(batch, m, n)
+    y_step = torch.empty_like(x)
+    capi.step(x, y_step, ws, a, b, c)
+    mp, gram_bytes = info.padded_rows, info.gram_bytes
+    p_off = -(-gram_bytes // 256) * 256
+    a_step = ws[:gram_bytes].clone()
+    p_step = ws[p_off:p_off + gram_bytes].clone()
+    gram = torch.empty(batch, mp, mp, dtype=torch.bfloat16, device=DEV)
+    poly = torch.empty_like(gram)
+    y = torch.empty_like(x)
+    capi.gram(x, gram, workspace=ws)
+    capi.poly(gram, poly, batch, m, n, b, c, workspace=ws)
+    capi.apply(poly, x, y, a, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(gram.view(torch.uint8).reshape(-1), a_step)
+    assert torch.equal(poly.view(torch.uint8).reshape(-1), p_step)
+    assert torch.equal(y, y_step)
+
+    x_np, y_ref = _exact_input(batch, m, n, seed=1000 + CASES.index(STAGE_CASES[case]))
+    xe = torch.from_numpy(x_np.astype(np.float32)).to(torch.bfloat16).to(DEV)
+    ye = torch.empty_like(xe)
+    capi.gram(xe, gram)
+    capi.poly(gram, poly, batch, m, n, *EXACT[1:])
+    capi.apply(poly, xe, ye, EXACT[0])
+    torch.cuda.synchronize()
+    got = ye.view(torch.int16).cpu().numpy().view(np.uint16)
+    want = O.f32_to_bf16_bits(y_ref.astype(np.float32))
+    assert np.array_equal(got, want)
