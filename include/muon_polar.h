@@ -237,6 +237,10 @@ typedef struct muon_polar_plan_extents {
     int64_t pad_end;
     int64_t y_bytes;          /* size of Y, the apply stage's output */
     muon_polar_stage_extent stage[3];
+    /* Rows that take the padded copy: the apply of a polar_express / Muon chain's
+       steps before the last, which writes its iterate padded to np columns (out_limit:
+       the padded buffer); all zero for other shapes. */
+    muon_polar_stage_extent chain_apply;
 } muon_polar_plan_extents;
 
 int muon_polar_check_plan(int64_t batch, int64_t m, int64_t n, int cus, const int *blocks_per_cu,

@@ -56,7 +56,7 @@ class PlanExtents(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int64) for name in (
         "workspace_bytes", "gram_bytes", "poly_offset", "counters_offset", "counter_stride",
         "partials_offset", "pad_offset", "pad_end", "y_bytes")] + [
-        ("stage", StageExtent * 3)]
+        ("stage", StageExtent * 3), ("chain_apply", StageExtent)]
 
 
 class CapiError(RuntimeError):

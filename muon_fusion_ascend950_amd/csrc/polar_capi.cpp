@@ -623,7 +623,10 @@ int build_plan(int64_t batch, int64_t m, int64_t n, const Knobs &knobs, const Ta
     p.workspace_bytes =
         p.pad_offset + (p.pad ? align256(static_cast<size_t>(batch) * m * p.np * 2u) : 0u);
     p.express_x_offset = p.workspace_bytes;
-    p.express_norm_offset = p.express_x_offset + align256(size_t(batch) * m * n * 2u);
+    // the chain's scratch iterate; with padded rows it holds a padded [batch, m, np]
+    // matrix (run_steps keeps the iterates of a chain padded between its steps)
+    p.express_norm_offset =
+        p.express_x_offset + align256(size_t(batch) * m * (p.pad ? p.np : n) * 2u);
     p.express_workspace_bytes =
         p.express_norm_offset +
         align256(size_t(batch) * muon_polar::norm_chunks(batch, m * n) * sizeof(float));
@@ -850,8 +853,11 @@ StageLaunch poly_launch(const Plan &p, const void *gram, void *poly, double b, d
 
 // x: [batch, m, n] rows `ldx` elements apart (n, or np for the padded copy);
 // y: [batch, m, n] dense.
+// n_out (>= n, default n): columns of Y written and its row length.  A padded Y
+// (n_out = np) gets the padded columns too, which come out +0 (X is zero there).
 StageLaunch apply_launch(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y,
-                         int64_t m, int64_t n, double a) {
+                         int64_t m, int64_t n, double a, int64_t n_out = 0) {
+    if (n_out <= 0) n_out = n;
     StageLaunch L{};
     GemmArgs &g = L.g;
     g.rowop = static_cast<const uint16_t *>(poly);
@@ -859,16 +865,16 @@ StageLaunch apply_launch(const Plan &p, const void *poly, const void *x, int64_t
     g.out = static_cast<uint16_t *>(y);
     g.sb_row = p.mp * p.mp;
     g.sb_col = g.sb_epi = m * ldx;
-    g.sb_out = m * n;
+    g.sb_out = m * n_out;
     g.ld_row = static_cast<int32_t>(p.mp);
     g.ld_col = g.ld_epi = static_cast<int32_t>(ldx);
-    g.ld_out = static_cast<int32_t>(n);
+    g.ld_out = static_cast<int32_t>(n_out);
     g.row_rows = g.row_k = static_cast<int32_t>(p.mp);
     g.col_rows = static_cast<int32_t>(n);
     g.col_k = static_cast<int32_t>(m);
     g.k_loop = static_cast<int32_t>(round_up(m, 64));  // P is zero beyond column m
     g.out_rows = static_cast<int32_t>(m);
-    g.out_cols = static_cast<int32_t>(n);
+    g.out_cols = static_cast<int32_t>(n_out);
     g.tiles_m = p.apply_tm;
     g.tiles_n = p.apply_tn;
     g.tiles_per_batch = p.apply_tm * p.apply_tn;
@@ -876,7 +882,7 @@ StageLaunch apply_launch(const Plan &p, const void *poly, const void *x, int64_t
     g.s_acc = 1.0f;
     L.extent[0] = p.mp * p.mp * 2;
     L.extent[1] = L.extent[2] = m * ldx * 2;
-    g.out_vec = (n % 8 == 0 && aligned16(y)) ? 1 : !aligned4(y) ? 0 : n % 2 == 0 ? 2 : 3;
+    g.out_vec = (n_out % 8 == 0 && aligned16(y)) ? 1 : !aligned4(y) ? 0 : n_out % 2 == 0 ? 2 : 3;
     g.group_n = apply_group(p);
     g.out_cpol = p.y_cpol;
     // DMA-fed kernel: X rows of whole 16-byte chunks (Y any alignment: 16-byte stores
@@ -1035,8 +1041,9 @@ int run_poly(const Plan &p, const void *gram, void *poly, int64_t batch, double 
 }
 
 int run_apply(const Plan &p, const void *poly, const void *x, int64_t ldx, void *y, int64_t batch,
-              int64_t m, int64_t n, double a, const SkArea *area, hipStream_t stream) {
-    StageLaunch L = apply_launch(p, poly, x, ldx, y, m, n, a);
+              int64_t m, int64_t n, double a, const SkArea *area, hipStream_t stream,
+              int64_t n_out = 0) {
+    StageLaunch L = apply_launch(p, poly, x, ldx, y, m, n, a, n_out);
     return launch_stage(L, batch, p, area, stream, "apply");
 }
 
@@ -1084,16 +1091,18 @@ int pad_input(const Plan &p, void *workspace, const void *x, int64_t batch, hipS
 // One step given the workspace: left form (m <= n) or right-Gram form; rows the
 // DMA-fed kernels cannot read in place are first copied into the zero-padded
 // buffer (pad_input).
+// ldx_in: row length of x (p.n, or p.np for an iterate a chain keeps padded); n_out:
+// row length of y (p.n, or p.np to keep the next iterate padded).
 int run_step(const Plan &p, const void *x, void *y, void *workspace, int64_t batch, double a,
-             double b, double c, hipStream_t stream) {
+             double b, double c, hipStream_t stream, int64_t ldx_in = 0, int64_t n_out = 0) {
     char *ws = static_cast<char *>(workspace);
     void *gram = ws;
     void *poly = ws + align256(p.gram_bytes);
     const SkArea areas[3] = {sk_area(p, workspace, 0), sk_area(p, workspace, 1),
                              sk_area(p, workspace, 2)};
     const void *xs = x;
-    int64_t ldx = p.n;
-    int st = pad_input(p, workspace, x, batch, stream, xs, ldx);
+    int64_t ldx = ldx_in > 0 ? ldx_in : p.n;
+    int st = ldx == p.n ? pad_input(p, workspace, x, batch, stream, xs, ldx) : MUON_POLAR_OK;
     if (st != MUON_POLAR_OK) return st;
     st = p.tall ? run_gram_t(p, xs, ldx, gram, batch, p.m, p.n, &areas[0], stream)
                 : run_gram(p, xs, ldx, gram, batch, p.m, p.n, &areas[0], stream);
@@ -1101,7 +1110,7 @@ int run_step(const Plan &p, const void *x, void *y, void *workspace, int64_t bat
     st = run_poly(p, gram, poly, batch, b, c, &areas[1], stream);
     if (st != MUON_POLAR_OK) return st;
     return p.tall ? run_apply_r(p, poly, xs, ldx, y, batch, p.m, p.n, a, &areas[2], stream)
-                  : run_apply(p, poly, xs, ldx, y, batch, p.m, p.n, a, &areas[2], stream);
+                  : run_apply(p, poly, xs, ldx, y, batch, p.m, p.n, a, &areas[2], stream, n_out);
 }
 
 // `steps` steps from `cur` (the normalised input, in the chain's first buffer),
@@ -1110,6 +1119,27 @@ int run_steps(const Plan &p, void *workspace, const uint16_t *cur, uint16_t *out
               uint16_t *scratch, int64_t batch, const double *coefficients, int64_t steps,
               hipStream_t stream) {
     if (steps == 0) return MUON_POLAR_OK;
+    if (steps >= 2 && !p.tall && pad_needed(p, cur)) {
+        // Rows the DMA-fed kernels cannot read in place (odd n): the first step pads
+        // its input into the workspace's padded buffer as every step does, but writes
+        // its result padded ([m, np], the padded columns +0) into the scratch iterate
+        // (sized for that), and every later step reads its input in place from one
+        // padded buffer and writes the other; only the last writes `out` at width n.
+        // The same values as padding each step's input: one padded copy per chain.
+        uint16_t *pads[2] = {
+            reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + p.pad_offset),
+            scratch};
+        for (int64_t i = 0; i < steps; ++i) {
+            const bool last = i == steps - 1;
+            const void *in = i == 0 ? static_cast<const void *>(cur) : pads[i % 2];
+            void *dst = last ? static_cast<void *>(out) : pads[(i + 1) % 2];
+            const int st = run_step(p, in, dst, workspace, batch, coefficients[3 * i],
+                                    coefficients[3 * i + 1], coefficients[3 * i + 2], stream,
+                                    i == 0 ? p.n : p.np, last ? p.n : p.np);
+            if (st != MUON_POLAR_OK) return st;
+        }
+        return MUON_POLAR_OK;
+    }
     for (int64_t i = 0; i < steps; ++i) {
         uint16_t *next = (steps - i - 1) % 2 == 0 ? out : scratch;
         const int st = run_step(p, cur, next, workspace, batch, coefficients[3 * i],
@@ -1665,6 +1695,19 @@ int muon_polar_check_plan(int64_t batch, int64_t m, int64_t n, int cus, const in
         out->stage[s].out_limit = s == 2 ? out->y_bytes : out->gram_bytes;
         out->stage[s].partial_limit = out->pad_offset - out->partials_offset;
         out->stage[s].counter_limit = p.counter_stride;
+    }
+    out->chain_apply = muon_polar_stage_extent{};
+    if (pad && !p.tall) {
+        // run_steps' inner steps: X and Y both padded (the padded buffer and the
+        // scratch iterate); Y's extent is the padded matrix
+        StageLaunch La = apply_launch(p, poly, xs, p.np, y, m, n, 1.0, p.np);
+        SkArea area{reinterpret_cast<float *>(ws + p.partials_offset),
+                    reinterpret_cast<uint64_t *>(ws + p.counters_offset) + 2 * p.counter_stride};
+        prepare_stage(La, batch, p, &area, 1u);
+        stage_extent(La, La.g.sk_units > 0, out->chain_apply);
+        out->chain_apply.out_limit = batch * m * p.np * 2;
+        out->chain_apply.partial_limit = out->pad_offset - out->partials_offset;
+        out->chain_apply.counter_limit = p.counter_stride;
     }
     return MUON_POLAR_OK;
 }

@@ -34,8 +34,12 @@ def check(plan: capi.PlanExtents) -> None:
     assert plan.partials_offset >= plan.counters_offset + 3 * plan.counter_stride * 8
     assert plan.pad_offset >= plan.partials_offset
     assert plan.pad_end <= plan.workspace_bytes
-    for s in range(3):
-        e = plan.stage[s]
+    # rows that take the padded copy (odd widths; even widths are read in place): a
+    # chain's inner steps write their iterate padded
+    chained = plan.chain_apply.total_tiles > 0
+    assert plan.pad_end > 0 or not chained
+    extents = [(s, plan.stage[s]) for s in range(3)] + ([(2, plan.chain_apply)] if chained else [])
+    for s, e in extents:
         assert e.coverage_ok == 1, f"stage {s}: an iteration is not computed exactly once"
         assert e.extents_ok == 1, f"stage {s}: an operand extent does not fit 32-bit offsets"
         assert 0 <= e.out_lo <= e.out_hi <= e.out_limit, (
@@ -59,6 +63,22 @@ def check(plan: capi.PlanExtents) -> None:
             # off-diagonal tiles and pairs of diagonal tiles, never cut
             assert s < 2 and e.dma_fed == 1 and (e.tile_m, e.tile_n, e.waves) == (64, 64, 4)
             assert e.sk_units == 0 and e.dp_tiles == e.total_tiles
+
+
+@pytest.mark.parametrize("shape", [(3, 129, 257), (2, 150, 2049), (1, 1000, 3001), (4, 64, 8191)])
+def test_padded_chain_apply_writes_the_whole_padded_iterate(shape):
+    """Odd widths: the apply of a chain's inner steps stores every column of the padded
+    iterate (its padded columns come out zero, the next step's padding) and nothing past
+    it, while the step's own apply stores up to column n."""
+    batch, m, n = shape
+    np_ = -(-n // 64) * 64
+    for occ in [(1, 1, 1), (2, 2, 2)]:
+        plan = capi.check_plan(*shape, cus=256, blocks_per_cu=occ)
+        check(plan)
+        assert plan.pad_end > 0 and plan.chain_apply.total_tiles > 0
+        assert plan.chain_apply.out_limit == batch * m * np_ * 2
+        assert plan.chain_apply.out_hi == batch * m * np_ * 2
+        assert plan.stage[2].out_hi == plan.y_bytes
 
 
 @pytest.mark.parametrize("occ", OCCUPANCIES)
