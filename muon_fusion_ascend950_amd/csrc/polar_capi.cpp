@@ -1074,9 +1074,11 @@ int check_tall(const Plan &p, const void *x, const void *y) {
 // and point (xs, ldx) at it; otherwise leave them at X.
 bool pad_needed(const Plan &p, const void *x) { return p.pad && !dma_rows(p.n, x); }
 
+// force: pad rows of n % 8 != 0 elements even where they could be read in place (a
+// chain's first step, which starts the chain's padded iterates).
 int pad_input(const Plan &p, void *workspace, const void *x, int64_t batch, hipStream_t stream,
-              const void *&xs, int64_t &ldx) {
-    if (!pad_needed(p, x)) return MUON_POLAR_OK;
+              const void *&xs, int64_t &ldx, bool force = false) {
+    if (!(pad_needed(p, x) || (force && p.pad))) return MUON_POLAR_OK;
     uint16_t *xp = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + p.pad_offset);
     const int st = finish_stage(
         muon_polar::launch_pad_rows(static_cast<const uint16_t *>(x), xp, batch * p.m, p.n, p.np,
@@ -1092,9 +1094,11 @@ int pad_input(const Plan &p, void *workspace, const void *x, int64_t batch, hipS
 // DMA-fed kernels cannot read in place are first copied into the zero-padded
 // buffer (pad_input).
 // ldx_in: row length of x (p.n, or p.np for an iterate a chain keeps padded); n_out:
-// row length of y (p.n, or p.np to keep the next iterate padded).
+// row length of y (p.n, or p.np to keep the next iterate padded); force_pad: copy x
+// into the padded buffer whenever its rows are not whole 16-byte chunks.
 int run_step(const Plan &p, const void *x, void *y, void *workspace, int64_t batch, double a,
-             double b, double c, hipStream_t stream, int64_t ldx_in = 0, int64_t n_out = 0) {
+             double b, double c, hipStream_t stream, int64_t ldx_in = 0, int64_t n_out = 0,
+             bool force_pad = false) {
     char *ws = static_cast<char *>(workspace);
     void *gram = ws;
     void *poly = ws + align256(p.gram_bytes);
@@ -1102,7 +1106,8 @@ int run_step(const Plan &p, const void *x, void *y, void *workspace, int64_t bat
                              sk_area(p, workspace, 2)};
     const void *xs = x;
     int64_t ldx = ldx_in > 0 ? ldx_in : p.n;
-    int st = ldx == p.n ? pad_input(p, workspace, x, batch, stream, xs, ldx) : MUON_POLAR_OK;
+    int st =
+        ldx == p.n ? pad_input(p, workspace, x, batch, stream, xs, ldx, force_pad) : MUON_POLAR_OK;
     if (st != MUON_POLAR_OK) return st;
     st = p.tall ? run_gram_t(p, xs, ldx, gram, batch, p.m, p.n, &areas[0], stream)
                 : run_gram(p, xs, ldx, gram, batch, p.m, p.n, &areas[0], stream);
@@ -1119,13 +1124,15 @@ int run_steps(const Plan &p, void *workspace, const uint16_t *cur, uint16_t *out
               uint16_t *scratch, int64_t batch, const double *coefficients, int64_t steps,
               hipStream_t stream) {
     if (steps == 0) return MUON_POLAR_OK;
-    if (steps >= 2 && !p.tall && pad_needed(p, cur)) {
-        // Rows the DMA-fed kernels cannot read in place (odd n): the first step pads
-        // its input into the workspace's padded buffer as every step does, but writes
-        // its result padded ([m, np], the padded columns +0) into the scratch iterate
-        // (sized for that), and every later step reads its input in place from one
-        // padded buffer and writes the other; only the last writes `out` at width n.
-        // The same values as padding each step's input: one padded copy per chain.
+    if (steps >= 2 && !p.tall && p.pad) {
+        // Rows that are not whole 16-byte chunks (n % 8 != 0): the first step pads its
+        // input into the workspace's padded buffer (as a single step does for odd n;
+        // even n it could read in place), but writes its result padded ([m, np], the
+        // padded columns +0) into the scratch iterate (sized for that), and every later
+        // step reads its input in place from one padded buffer and writes the other;
+        // only the last writes `out` at width n.  The same values as padding (or
+        // masking) each step's input: one copy per chain, and the inner steps read
+        // aligned rows and store whole chunks.
         uint16_t *pads[2] = {
             reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + p.pad_offset),
             scratch};
@@ -1135,7 +1142,7 @@ int run_steps(const Plan &p, void *workspace, const uint16_t *cur, uint16_t *out
             void *dst = last ? static_cast<void *>(out) : pads[(i + 1) % 2];
             const int st = run_step(p, in, dst, workspace, batch, coefficients[3 * i],
                                     coefficients[3 * i + 1], coefficients[3 * i + 2], stream,
-                                    i == 0 ? p.n : p.np, last ? p.n : p.np);
+                                    i == 0 ? p.n : p.np, last ? p.n : p.np, true);
             if (st != MUON_POLAR_OK) return st;
         }
         return MUON_POLAR_OK;
@@ -1697,10 +1704,10 @@ int muon_polar_check_plan(int64_t batch, int64_t m, int64_t n, int cus, const in
         out->stage[s].counter_limit = p.counter_stride;
     }
     out->chain_apply = muon_polar_stage_extent{};
-    if (pad && !p.tall) {
+    if (p.pad && !p.tall) {
         // run_steps' inner steps: X and Y both padded (the padded buffer and the
         // scratch iterate); Y's extent is the padded matrix
-        StageLaunch La = apply_launch(p, poly, xs, p.np, y, m, n, 1.0, p.np);
+        StageLaunch La = apply_launch(p, poly, ws + p.pad_offset, p.np, y, m, n, 1.0, p.np);
         SkArea area{reinterpret_cast<float *>(ws + p.partials_offset),
                     reinterpret_cast<uint64_t *>(ws + p.counters_offset) + 2 * p.counter_stride};
         prepare_stage(La, batch, p, &area, 1u);

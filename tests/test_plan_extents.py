@@ -34,8 +34,8 @@ def check(plan: capi.PlanExtents) -> None:
     assert plan.partials_offset >= plan.counters_offset + 3 * plan.counter_stride * 8
     assert plan.pad_offset >= plan.partials_offset
     assert plan.pad_end <= plan.workspace_bytes
-    # rows that take the padded copy (odd widths; even widths are read in place): a
-    # chain's inner steps write their iterate padded
+    # rows of n % 8 != 0 elements (a padded buffer in the workspace): a chain's inner
+    # steps write their iterate padded
     chained = plan.chain_apply.total_tiles > 0
     assert plan.pad_end > 0 or not chained
     extents = [(s, plan.stage[s]) for s in range(3)] + ([(2, plan.chain_apply)] if chained else [])
@@ -65,11 +65,12 @@ def check(plan: capi.PlanExtents) -> None:
             assert e.sk_units == 0 and e.dp_tiles == e.total_tiles
 
 
-@pytest.mark.parametrize("shape", [(3, 129, 257), (2, 150, 2049), (1, 1000, 3001), (4, 64, 8191)])
+@pytest.mark.parametrize("shape", [(3, 129, 257), (2, 150, 2049), (1, 1000, 3001), (4, 64, 8191),
+                                   (2, 150, 2050), (1, 129, 130), (3, 200, 1002)])
 def test_padded_chain_apply_writes_the_whole_padded_iterate(shape):
-    """Odd widths: the apply of a chain's inner steps stores every column of the padded
-    iterate (its padded columns come out zero, the next step's padding) and nothing past
-    it, while the step's own apply stores up to column n."""
+    """n % 8 != 0 (odd and even): the apply of a chain's inner steps stores every column
+    of the padded iterate (its padded columns come out zero, the next step's padding) and
+    nothing past it, while the step's own apply stores up to column n."""
     batch, m, n = shape
     np_ = -(-n // 64) * 64
     for occ in [(1, 1, 1), (2, 2, 2)]:
